@@ -1,0 +1,1184 @@
+// ds3_hip.cpp -- host runtime of the MI355X MoE-FFN backend (C ABI in
+// include/ds3_hip.h).  One device context, one stream, opaque buffers, a
+// growable device workspace, and the entry points that validate arguments
+// like the reference's Metal host (src/ds3_metal.m:373-449, 1841-1862,
+// 2172-2828) and enqueue the gfx950 kernels.
+#include "ds3_hip.h"
+#include "kernels/launch.h"
+
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <unistd.h>
+#include <vector>
+
+struct ds3_hip_buffer {
+    uint8_t *base;      // device allocation (shared by views)
+    size_t bytes;       // bytes visible through this handle
+    size_t offset;      // byte offset of this handle inside base
+    bool owner;         // frees base on ds3_hip_buffer_free
+    bool readonly;      // from_mmap buffers refuse writes
+};
+
+using namespace ds3k;
+
+namespace {
+
+constexpr int kDefaultPrefillMin = 16;
+constexpr size_t kAllocPad = 256;        // slack after every allocation: kernels read whole dwords
+
+struct KRec {
+    const char *name;
+    int e0, e1;
+};
+
+struct State {
+    bool inited = false;
+    hipStream_t stream = nullptr;
+    bool batch = false;
+    uint8_t *ws = nullptr;
+    size_t ws_bytes = 0;
+    int32_t *zero_idx = nullptr;     // device {0}
+    float *one_f = nullptr;          // device {1.0f}
+    int32_t *guard = nullptr;        // device guard counter
+    int prefill_min = kDefaultPrefillMin;
+    // reference-style profiling (src/ds3_metal.m:2868-2885)
+    bool profile = false;
+    int cb_count = 0;
+    double gpu_ms = 0.0, cpu_ms = 0.0;
+    hipEvent_t bev0 = nullptr, bev1 = nullptr;
+    // per-kernel timing
+    bool ktiming = false;
+    std::vector<hipEvent_t> pool;
+    int pool_used = 0;
+    std::vector<KRec> recs;
+    std::vector<std::string> stat_names;
+    std::vector<int64_t> stat_count;
+    std::vector<double> stat_ms;
+    bool stats_dirty = true;
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+};
+
+State g;
+
+void *dptr(const ds3_hip_buffer_t *b) { return b ? (void *)(b->base + b->offset) : nullptr; }
+const uint8_t *cptr(const ds3_hip_buffer_t *b) { return b ? b->base + b->offset : nullptr; }
+float *fptr(const ds3_hip_buffer_t *b) { return (float *)dptr(b); }
+
+bool ensure_init()
+{
+    if (g.inited) return true;
+    return ds3_hip_init() == 0;
+}
+
+int report(hipError_t e, const char *what)
+{
+    if (e == hipSuccess) return 0;
+    fprintf(stderr, "ds3_hip: %s failed: %s\n", what, hipGetErrorString(e));
+    return -1;
+}
+
+// Complete an entry point: surface launch errors, and outside a batch wait
+// for the stream (calls are synchronous there, as in the reference).
+int finish(hipError_t e, const char *what)
+{
+    if (report(e, what) != 0) return -1;
+    if (!g.batch) return report(hipStreamSynchronize(g.stream), what);
+    return 0;
+}
+
+// Device workspace, grown on demand.  Growing waits for queued work that may
+// still use the old block.
+uint8_t *ws_get(size_t bytes)
+{
+    if (bytes <= g.ws_bytes) return g.ws;
+    if (g.ws) {
+        (void)hipStreamSynchronize(g.stream);
+        (void)hipFree(g.ws);
+        g.ws = nullptr;
+        g.ws_bytes = 0;
+    }
+    const size_t want = bytes + bytes / 4 + (1u << 20);
+    if (hipMalloc((void **)&g.ws, want) != hipSuccess) {
+        fprintf(stderr, "ds3_hip: workspace allocation of %zu bytes failed\n", want);
+        g.ws = nullptr;
+        return nullptr;
+    }
+    g.ws_bytes = want;
+    return g.ws;
+}
+
+struct Bump {
+    size_t off = 0;
+    size_t take(size_t bytes)
+    {
+        const size_t o = off;
+        off = (off + bytes + 255) & ~(size_t)255;
+        return o;
+    }
+};
+
+// RAII event pair around one kernel launch while kernel timing is on.
+struct KScope {
+    int e0 = -1;
+    const char *name;
+    explicit KScope(const char *n) : name(n)
+    {
+        if (g.ktiming && g.pool_used + 2 <= (int)g.pool.size()) {
+            e0 = g.pool_used;
+            g.pool_used += 2;
+            (void)hipEventRecord(g.pool[e0], g.stream);
+        }
+    }
+    ~KScope()
+    {
+        if (e0 >= 0) {
+            (void)hipEventRecord(g.pool[e0 + 1], g.stream);
+            g.recs.push_back({ name, e0, e0 + 1 });
+            g.stats_dirty = true;
+        }
+    }
+};
+
+bool is_quant(int t) { return t == T_Q4_K || t == T_Q6_K || t == T_Q8_0; }
+
+// reference src/ds3_metal.m:1841-1862
+bool quant_type_ok_for_moe(int type, uint32_t in_dim, const char *name)
+{
+    if (type == T_F32) {
+        if (in_dim % 32 != 0) {
+            fprintf(stderr, "ds3_hip: %s F32 requires in_dim=%u multiple of 32\n", name, in_dim);
+            return false;
+        }
+        return true;
+    }
+    if (type == T_Q4_K || type == T_Q6_K) {
+        if (in_dim % 256 != 0) {
+            fprintf(stderr, "ds3_hip: %s type=%d requires in_dim=%u multiple of 256\n", name, type, in_dim);
+            return false;
+        }
+        return true;
+    }
+    if (type == T_Q8_0) {
+        if (in_dim % 32 != 0) {
+            fprintf(stderr, "ds3_hip: %s type=%d requires in_dim=%u multiple of 32\n", name, type, in_dim);
+            return false;
+        }
+        return true;
+    }
+    fprintf(stderr, "ds3_hip: unsupported %s type %d\n", name, type);
+    return false;
+}
+
+bool fits(const ds3_hip_buffer_t *b, size_t need, const char *what)
+{
+    if (!b) return true;
+    if (b->bytes < need) {
+        fprintf(stderr, "ds3_hip: buffer %s holds %zu bytes, needs %zu\n", what, b->bytes, need);
+        return false;
+    }
+    return true;
+}
+
+// Per-token expert products for `slots` routed slots of T tokens:
+// h = swiglu(gate, up) then out (+)= sum_k w_k * down(h_k).
+int run_experts_decode(const float *x, int64_t ldx, const int32_t *idx, const float *wts, int T, int n_used,
+                       const ExpertWeights &ew, uint32_t n_embd, uint32_t n_ff, float *out, const float *residual,
+                       bool accumulate, float *h, float *tmp_up)
+{
+    const int slots = T * n_used;
+    hipError_t e;
+    if (ew.gate_type == ew.up_type) {
+        KScope ks("moe_decode_gate_up");
+        e = launch_decode_gate_up(x, ldx, idx, slots, n_used, ew, (int)n_embd, (int)n_ff, h, g.stream);
+    } else {
+        // Mismatched gate/up types: two projections, then silu_mul
+        // (the reference's unfused fallback, src/ds3_metal.m:2107-2140).
+        ExpertWeights eg = ew, eu = ew;
+        eg.up = ew.gate; eg.up_type = ew.gate_type; eg.up_stride = ew.gate_stride;
+        eu.gate = ew.up; eu.gate_type = ew.up_type; eu.gate_stride = ew.up_stride;
+        KScope ks("moe_decode_proj");
+        e = launch_decode_proj(x, ldx, idx, slots, n_used, eg, 0, (int)n_embd, (int)n_ff, h, g.stream);
+        if (e == hipSuccess)
+            e = launch_decode_proj(x, ldx, idx, slots, n_used, eu, 1, (int)n_embd, (int)n_ff, tmp_up, g.stream);
+        if (e == hipSuccess) e = launch_silu_mul(h, tmp_up, h, (int64_t)slots * n_ff, g.stream);
+    }
+    if (e != hipSuccess) return report(e, "decode gate/up");
+    KScope ks("moe_decode_down");
+    e = launch_decode_down(h, idx, wts, T, n_used, ew, (int)n_embd, (int)n_ff, out, n_embd, residual, accumulate,
+                           g.stream);
+    return report(e, "decode down");
+}
+
+}  // namespace
+
+// ===========================================================================
+// Lifecycle
+// ===========================================================================
+
+extern "C" int ds3_hip_init(void)
+{
+    if (g.inited) return 0;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        fprintf(stderr, "ds3_hip: no HIP device available\n");
+        return -1;
+    }
+    if (hipSetDevice(0) != hipSuccess) return -1;
+    if (hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking) != hipSuccess) {
+        fprintf(stderr, "ds3_hip: stream creation failed\n");
+        return -1;
+    }
+    void *consts = nullptr;
+    if (hipMalloc(&consts, 256) != hipSuccess) return -1;
+    g.zero_idx = (int32_t *)consts;
+    g.one_f = (float *)((uint8_t *)consts + 64);
+    g.guard = (int32_t *)((uint8_t *)consts + 128);
+    const int32_t zi = 0;
+    const float one = 1.0f;
+    (void)hipMemcpy(g.zero_idx, &zi, sizeof zi, hipMemcpyHostToDevice);
+    (void)hipMemcpy(g.one_f, &one, sizeof one, hipMemcpyHostToDevice);
+    (void)hipMemset(g.guard, 0, sizeof(int32_t));
+    (void)hipEventCreate(&g.bev0);
+    (void)hipEventCreate(&g.bev1);
+    (void)hipEventCreate(&g.t0);
+    (void)hipEventCreate(&g.t1);
+    const char *p = getenv("DS3_HIP_PROFILE");
+    g.profile = p && *p && *p != '0';
+    g.inited = true;
+    return 0;
+}
+
+extern "C" void ds3_hip_shutdown(void)
+{
+    if (!g.inited) return;
+    (void)hipStreamSynchronize(g.stream);
+    for (hipEvent_t e : g.pool) (void)hipEventDestroy(e);
+    g.pool.clear();
+    g.recs.clear();
+    (void)hipEventDestroy(g.bev0);
+    (void)hipEventDestroy(g.bev1);
+    (void)hipEventDestroy(g.t0);
+    (void)hipEventDestroy(g.t1);
+    if (g.ws) (void)hipFree(g.ws);
+    (void)hipFree(g.zero_idx);
+    (void)hipStreamDestroy(g.stream);
+    g = State();
+}
+
+// ===========================================================================
+// Buffers (reference src/ds3_metal.m:373-449)
+// ===========================================================================
+
+extern "C" ds3_hip_buffer_t *ds3_hip_buffer_alloc(size_t bytes)
+{
+    if (bytes == 0 || !ensure_init()) return nullptr;
+    void *p = nullptr;
+    const size_t padded = ((bytes + 255) & ~(size_t)255) + kAllocPad;
+    if (hipMalloc(&p, padded) != hipSuccess) return nullptr;
+    (void)hipMemset(p, 0, padded);
+    auto *b = (ds3_hip_buffer_t *)calloc(1, sizeof(ds3_hip_buffer_t));
+    if (!b) {
+        (void)hipFree(p);
+        return nullptr;
+    }
+    *b = { (uint8_t *)p, bytes, 0, true, false };
+    return b;
+}
+
+extern "C" ds3_hip_buffer_t *ds3_hip_buffer_from_mmap(const void *base, size_t bytes)
+{
+    if (!base || bytes == 0) return nullptr;
+    long ps = sysconf(_SC_PAGESIZE);
+    if (ps <= 0) ps = 4096;
+    if (((uintptr_t)base) & ((uintptr_t)ps - 1)) {
+        fprintf(stderr, "ds3_hip: mmap base %p is not page-aligned\n", base);
+        return nullptr;
+    }
+    ds3_hip_buffer_t *b = ds3_hip_buffer_alloc(bytes);
+    if (!b) return nullptr;
+    if (hipMemcpy(b->base, base, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+        ds3_hip_buffer_free(b);
+        return nullptr;
+    }
+    b->readonly = true;
+    return b;
+}
+
+extern "C" ds3_hip_buffer_t *ds3_hip_buffer_view(const ds3_hip_buffer_t *base, size_t offset, size_t bytes)
+{
+    if (!base || !base->base || offset > base->bytes || bytes == 0 || offset + bytes > base->bytes) return nullptr;
+    auto *v = (ds3_hip_buffer_t *)calloc(1, sizeof(ds3_hip_buffer_t));
+    if (!v) return nullptr;
+    *v = { base->base, bytes, base->offset + offset, false, base->readonly };
+    return v;
+}
+
+extern "C" void ds3_hip_buffer_free(ds3_hip_buffer_t *buf)
+{
+    if (!buf) return;
+    if (buf->owner && buf->base) {
+        if (g.inited) (void)hipStreamSynchronize(g.stream);
+        (void)hipFree(buf->base);
+    }
+    free(buf);
+}
+
+extern "C" int ds3_hip_buffer_write(ds3_hip_buffer_t *buf, size_t offset, const void *src, size_t bytes)
+{
+    if (!buf || !src || offset + bytes > buf->bytes || buf->readonly) return -1;
+    if (bytes == 0) return 0;
+    hipError_t e = hipMemcpyAsync(buf->base + buf->offset + offset, src, bytes, hipMemcpyHostToDevice, g.stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g.stream);
+    return report(e, "buffer_write");
+}
+
+extern "C" int ds3_hip_buffer_read(ds3_hip_buffer_t *buf, size_t offset, void *dst, size_t bytes)
+{
+    if (!buf || !dst || offset + bytes > buf->bytes) return -1;
+    if (bytes == 0) return 0;
+    hipError_t e = hipMemcpyAsync(dst, buf->base + buf->offset + offset, bytes, hipMemcpyDeviceToHost, g.stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(g.stream);
+    return report(e, "buffer_read");
+}
+
+// ===========================================================================
+// Products
+// ===========================================================================
+
+static int vec_matmul_typed(const ds3_hip_buffer_t *x, const ds3_hip_buffer_t *W, ds3_hip_buffer_t *y,
+                            uint32_t in_dim, uint32_t out_dim, uint64_t row_stride, int type, const char *what)
+{
+    if (!x || !W || !y || !ensure_init()) return -1;
+    if (!gemv_type_ok(type, (int)in_dim)) {
+        fprintf(stderr, "ds3_hip: %s type=%d in_dim=%u unsupported\n", what, type, in_dim);
+        return -1;
+    }
+    if (!fits(x, (size_t)in_dim * 4, "x") || !fits(y, (size_t)out_dim * 4, "y") ||
+        !fits(W, (size_t)(out_dim - 1) * row_stride + (size_t)row_stride, "W"))
+        return -1;
+    KScope ks("gemv");
+    return finish(launch_gemv(type, (const float *)dptr(x), in_dim, cptr(W), row_stride, fptr(y), out_dim, 1,
+                              (int)out_dim, (int)in_dim, nullptr, g.stream),
+                  what);
+}
+
+extern "C" int ds3_hip_vec_matmul_f32(const ds3_hip_buffer_t *x, const ds3_hip_buffer_t *W, ds3_hip_buffer_t *y,
+                                      uint32_t in_dim, uint32_t out_dim, uint64_t row_stride)
+{
+    if (row_stride < (uint64_t)in_dim * 4) {
+        fprintf(stderr, "ds3_hip: vec_matmul_f32 row_stride=%llu < in_dim*4\n", (unsigned long long)row_stride);
+        return -1;
+    }
+    return vec_matmul_typed(x, W, y, in_dim, out_dim, row_stride, T_F32, "vec_matmul_f32");
+}
+
+extern "C" int ds3_hip_vec_matmul_quantized(const ds3_hip_buffer_t *x, const ds3_hip_buffer_t *W, ds3_hip_buffer_t *y,
+                                            uint32_t in_dim, uint32_t out_dim, uint64_t row_stride,
+                                            ds3_hip_type_t type)
+{
+    if (!x || !W || !y) return -1;
+    if (type == T_Q4_K || type == T_Q6_K) {
+        if (in_dim % 256 != 0) {
+            fprintf(stderr, "ds3_hip: type %d in_dim=%u must be a multiple of 256\n", type, in_dim);
+            return -1;
+        }
+    } else if (type == T_Q8_0) {
+        if (in_dim % 32 != 0) {
+            fprintf(stderr, "ds3_hip: Q8_0 in_dim=%u must be a multiple of 32\n", in_dim);
+            return -1;
+        }
+    } else {
+        fprintf(stderr, "ds3_hip: unsupported quantized matmul type %d\n", type);
+        return -1;
+    }
+    return vec_matmul_typed(x, W, y, in_dim, out_dim, row_stride, type, "vec_matmul_quantized");
+}
+
+extern "C" int ds3_hip_vec_matmul_f32_simd(const ds3_hip_buffer_t *x, const ds3_hip_buffer_t *W, ds3_hip_buffer_t *y,
+                                           uint32_t in_dim, uint32_t out_dim, uint64_t row_stride)
+{
+    return ds3_hip_vec_matmul_f32(x, W, y, in_dim, out_dim, row_stride);
+}
+
+extern "C" int ds3_hip_vec_matmul_q8_0_simd(const ds3_hip_buffer_t *x, const ds3_hip_buffer_t *W, ds3_hip_buffer_t *y,
+                                            uint32_t in_dim, uint32_t out_dim, uint64_t row_stride)
+{
+    return ds3_hip_vec_matmul_quantized(x, W, y, in_dim, out_dim, row_stride, T_Q8_0);
+}
+
+extern "C" int ds3_hip_vec_matmul_q4k_simd(const ds3_hip_buffer_t *x, const ds3_hip_buffer_t *W, ds3_hip_buffer_t *y,
+                                           uint32_t in_dim, uint32_t out_dim, uint64_t row_stride)
+{
+    return ds3_hip_vec_matmul_quantized(x, W, y, in_dim, out_dim, row_stride, T_Q4_K);
+}
+
+extern "C" int ds3_hip_vec_matmul_q6k_simd(const ds3_hip_buffer_t *x, const ds3_hip_buffer_t *W, ds3_hip_buffer_t *y,
+                                           uint32_t in_dim, uint32_t out_dim, uint64_t row_stride)
+{
+    return ds3_hip_vec_matmul_quantized(x, W, y, in_dim, out_dim, row_stride, T_Q6_K);
+}
+
+// reference src/ds3_metal.m:2741-2828
+extern "C" int ds3_hip_matmul_quantized_batch(const ds3_hip_buffer_t *A, const ds3_hip_buffer_t *W,
+                                              ds3_hip_buffer_t *C, uint32_t M, uint32_t N, uint32_t K,
+                                              uint64_t weight_row_stride, uint64_t weight_offset,
+                                              ds3_hip_type_t type)
+{
+    if (!A || !W || !C || !ensure_init()) return -1;
+    if (type == T_Q4_K || type == T_Q6_K) {
+        if (K % 256 != 0) {
+            fprintf(stderr, "ds3_hip: type %d batch K=%u must be a multiple of 256\n", type, K);
+            return -1;
+        }
+    } else if (type == T_Q8_0) {
+        if (K % 32 != 0) {
+            fprintf(stderr, "ds3_hip: Q8_0 batch K=%u must be a multiple of 32\n", K);
+            return -1;
+        }
+    } else {
+        fprintf(stderr, "ds3_hip: unsupported quantized batch matmul type %d\n", type);
+        return -1;
+    }
+    if (M == 0 || N == 0) return 0;
+    if (!fits(A, (size_t)M * K * 4, "A") || !fits(C, (size_t)M * N * 4, "C") ||
+        !fits(W, weight_offset + (size_t)N * weight_row_stride, "W"))
+        return -1;
+    KScope ks("gemv");
+    return finish(launch_gemv(type, fptr(A), K, cptr(W) + weight_offset, weight_row_stride, fptr(C), N, (int)M,
+                              (int)N, (int)K, nullptr, g.stream),
+                  "matmul_quantized_batch");
+}
+
+// ===========================================================================
+// Elementwise (reference src/ds3_metal.m:994-1103)
+// ===========================================================================
+
+extern "C" int ds3_hip_buffer_copy_f32(const ds3_hip_buffer_t *src, ds3_hip_buffer_t *dst, size_t bytes)
+{
+    if (!src || !dst || bytes == 0 || !ensure_init()) return -1;
+    if (bytes % sizeof(float) != 0) {
+        fprintf(stderr, "ds3_hip: buffer_copy_f32 bytes=%zu must be a multiple of %zu\n", bytes, sizeof(float));
+        return -1;
+    }
+    if (!fits(src, bytes, "src") || !fits(dst, bytes, "dst")) return -1;
+    KScope ks("copy");
+    return finish(launch_copy(fptr(src), fptr(dst), (int64_t)(bytes / 4), g.stream), "buffer_copy_f32");
+}
+
+extern "C" int ds3_hip_buffer_zero_f32(ds3_hip_buffer_t *buf, size_t bytes)
+{
+    if (!buf || bytes == 0 || !ensure_init()) return -1;
+    if (bytes % sizeof(float) != 0) {
+        fprintf(stderr, "ds3_hip: buffer_zero_f32 bytes=%zu must be a multiple of %zu\n", bytes, sizeof(float));
+        return -1;
+    }
+    if (!fits(buf, bytes, "buf")) return -1;
+    KScope ks("zero");
+    return finish(launch_fill_zero(fptr(buf), (int64_t)(bytes / 4), g.stream), "buffer_zero_f32");
+}
+
+extern "C" int ds3_hip_vec_add_inplace(ds3_hip_buffer_t *acc, const ds3_hip_buffer_t *addend, uint32_t n)
+{
+    if (!acc || !addend || !ensure_init()) return -1;
+    if (n == 0) return 0;
+    if (!fits(acc, (size_t)n * 4, "acc") || !fits(addend, (size_t)n * 4, "addend")) return -1;
+    KScope ks("add");
+    return finish(launch_add(fptr(acc), fptr(addend), fptr(acc), n, g.stream), "vec_add_inplace");
+}
+
+extern "C" int ds3_hip_vec_add(const ds3_hip_buffer_t *a, const ds3_hip_buffer_t *b, ds3_hip_buffer_t *c, uint32_t n)
+{
+    if (!a || !b || !c || !ensure_init()) return -1;
+    if (n == 0) return 0;
+    if (!fits(a, (size_t)n * 4, "a") || !fits(b, (size_t)n * 4, "b") || !fits(c, (size_t)n * 4, "c")) return -1;
+    KScope ks("add");
+    return finish(launch_add(fptr(a), fptr(b), fptr(c), n, g.stream), "vec_add");
+}
+
+extern "C" int ds3_hip_gather_rows_f32(const ds3_hip_buffer_t *src, const ds3_hip_buffer_t *ids, ds3_hip_buffer_t *dst,
+                                       uint32_t n_cols, uint32_t count, uint32_t offset)
+{
+    if (!src || !ids || !dst || n_cols == 0 || count == 0 || !ensure_init()) return -1;
+    if (!fits(ids, ((size_t)offset + count) * 4, "ids") || !fits(dst, (size_t)count * n_cols * 4, "dst")) return -1;
+    KScope ks("gather_rows");
+    return finish(launch_gather_rows(fptr(src), (const int32_t *)dptr(ids) + offset, fptr(dst), (int)n_cols,
+                                     (int)count, (int64_t)(src->bytes / ((size_t)n_cols * 4)), g.stream),
+                  "gather_rows_f32");
+}
+
+extern "C" int ds3_hip_scatter_add_weighted_f32(const ds3_hip_buffer_t *src, const ds3_hip_buffer_t *scores,
+                                                const ds3_hip_buffer_t *ids, ds3_hip_buffer_t *dst, uint32_t n_cols,
+                                                uint32_t count, uint32_t offset)
+{
+    if (!src || !scores || !ids || !dst || n_cols == 0 || count == 0 || !ensure_init()) return -1;
+    if (!fits(ids, ((size_t)offset + count) * 4, "ids") || !fits(scores, ((size_t)offset + count) * 4, "scores") ||
+        !fits(src, (size_t)count * n_cols * 4, "src"))
+        return -1;
+    KScope ks("scatter_add");
+    return finish(launch_scatter_add(fptr(src), fptr(scores) + offset, (const int32_t *)dptr(ids) + offset,
+                                     fptr(dst), (int)n_cols, (int)count, (int64_t)(dst->bytes / ((size_t)n_cols * 4)),
+                                     g.stream),
+                  "scatter_add_weighted_f32");
+}
+
+extern "C" int ds3_hip_silu_mul_f32(const ds3_hip_buffer_t *gate, const ds3_hip_buffer_t *up, ds3_hip_buffer_t *out,
+                                    uint32_t n)
+{
+    if (!gate || !up || !out || !ensure_init()) return -1;
+    if (n == 0) return 0;
+    if (!fits(gate, (size_t)n * 4, "gate") || !fits(up, (size_t)n * 4, "up") || !fits(out, (size_t)n * 4, "out"))
+        return -1;
+    KScope ks("silu_mul");
+    return finish(launch_silu_mul(fptr(gate), fptr(up), fptr(out), n, g.stream), "silu_mul_f32");
+}
+
+// ===========================================================================
+// MoE
+// ===========================================================================
+
+namespace {
+
+ExpertWeights make_ew(const ds3_hip_buffer_t *wg, const ds3_hip_buffer_t *wu, const ds3_hip_buffer_t *wd, int gt,
+                      int ut, int dt, uint64_t gs, uint64_t us, uint64_t ds, const ds3_hip_buffer_t *table)
+{
+    ExpertWeights ew;
+    ew.gate = cptr(wg);
+    ew.up = cptr(wu);
+    ew.down = cptr(wd);
+    ew.gate_stride = gs;
+    ew.up_stride = us;
+    ew.down_stride = ds;
+    ew.gate_type = gt;
+    ew.up_type = ut;
+    ew.down_type = dt;
+    ew.table = table ? (const uint64_t *)dptr(table) : nullptr;
+    return ew;
+}
+
+// Shared expert, weight 1, accumulated into out (reference src/ds3_metal.m:2227-2243).
+int run_shared(const float *x, const ds3_hip_buffer_t *sg, const ds3_hip_buffer_t *su, const ds3_hip_buffer_t *sd,
+               int sgt, int sut, int sdt, uint64_t sgs, uint64_t sus, uint64_t sds, uint32_t n_embd,
+               uint32_t n_ff_shared, float *out, float *h, float *tmp)
+{
+    ExpertWeights ew = make_ew(sg, su, sd, sgt, sut, sdt, sgs, sus, sds, nullptr);
+    return run_experts_decode(x, n_embd, g.zero_idx, g.one_f, 1, 1, ew, n_embd, n_ff_shared, out, nullptr, true, h,
+                              tmp);
+}
+
+bool moe_limits_ok(uint32_t n_expert, uint32_t n_used)
+{
+    if (n_expert > 256 || n_used > 16) {
+        fprintf(stderr, "ds3_hip: n_expert=%u (max 256) / n_used=%u (max 16) out of range\n", n_expert, n_used);
+        return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+// reference src/ds3_metal.m:2415-2661
+extern "C" int ds3_hip_moe_ffn(
+    const ds3_hip_buffer_t *input, const ds3_hip_buffer_t *w_gate_inp, const ds3_hip_buffer_t *w_gate_exps,
+    const ds3_hip_buffer_t *w_up_exps, const ds3_hip_buffer_t *w_down_exps, ds3_hip_type_t gate_type,
+    ds3_hip_type_t up_type, ds3_hip_type_t down_type, uint64_t gate_row_stride, uint64_t up_row_stride,
+    uint64_t down_row_stride, const ds3_hip_buffer_t *w_shared_gate, const ds3_hip_buffer_t *w_shared_up,
+    const ds3_hip_buffer_t *w_shared_down, ds3_hip_type_t shared_gate_type, ds3_hip_type_t shared_up_type,
+    ds3_hip_type_t shared_down_type, uint64_t shared_gate_row_stride, uint64_t shared_up_row_stride,
+    uint64_t shared_down_row_stride, ds3_hip_buffer_t *output, ds3_hip_buffer_t *gate_logits,
+    const ds3_hip_buffer_t *expert_offsets, ds3_hip_buffer_t *hidden, ds3_hip_buffer_t *expert_up,
+    ds3_hip_buffer_t *expert_down, uint32_t n_embd, uint32_t n_expert, uint32_t n_used, uint32_t n_ff_exp,
+    uint32_t n_ff_shared, uint64_t router_row_stride, ds3_hip_type_t router_type, bool norm_topk_prob)
+{
+    const bool has_shared = w_shared_gate && w_shared_up && w_shared_down;
+    if (!input || !w_gate_inp || !w_gate_exps || !w_up_exps || !w_down_exps || !output || !gate_logits || !hidden)
+        return -1;
+    if (!quant_type_ok_for_moe(gate_type, n_embd, "gate") || !quant_type_ok_for_moe(up_type, n_embd, "up") ||
+        !quant_type_ok_for_moe(down_type, n_ff_exp, "down"))
+        return -1;
+    if (has_shared && (!quant_type_ok_for_moe(shared_gate_type, n_embd, "shared_gate") ||
+                       !quant_type_ok_for_moe(shared_up_type, n_embd, "shared_up") ||
+                       !quant_type_ok_for_moe(shared_down_type, n_ff_shared, "shared_down")))
+        return -1;
+    const bool routed_q = is_quant(gate_type) || is_quant(up_type) || is_quant(down_type);
+    const bool shared_q =
+        has_shared && (is_quant(shared_gate_type) || is_quant(shared_up_type) || is_quant(shared_down_type));
+    if ((routed_q || shared_q) && (!expert_up || !expert_down)) {
+        fprintf(stderr, "ds3_hip: quantized MoE path requires expert_up/expert_down scratch buffers\n");
+        return -1;
+    }
+    if (n_embd == 0 || n_expert == 0 || n_used == 0 || n_ff_exp == 0) return -1;
+    if (n_used > n_expert) return -1;
+    if (!moe_limits_ok(n_expert, n_used) || !gemv_type_ok(router_type, (int)n_embd) || !ensure_init()) {
+        if (!gemv_type_ok(router_type, (int)n_embd))
+            fprintf(stderr, "ds3_hip: router type %d with n_embd=%u unsupported\n", router_type, n_embd);
+        return -1;
+    }
+    if (!fits(input, (size_t)n_embd * 4, "input") || !fits(output, (size_t)n_embd * 4, "output") ||
+        !fits(gate_logits, (size_t)n_expert * 4, "gate_logits"))
+        return -1;
+
+    const uint32_t ff_max = has_shared && n_ff_shared > n_ff_exp ? n_ff_shared : n_ff_exp;
+    Bump bp;
+    const size_t o_idx = bp.take((size_t)n_used * 4), o_sc = bp.take((size_t)n_used * 4);
+    const size_t o_wn = bp.take((size_t)n_expert * 4);
+    const size_t o_h = bp.take((size_t)n_used * ff_max * 4), o_t = bp.take((size_t)n_used * ff_max * 4);
+    uint8_t *ws = ws_get(bp.off);
+    if (!ws) return -1;
+    int32_t *idx = (int32_t *)(ws + o_idx);
+    float *sc = (float *)(ws + o_sc), *wn = (float *)(ws + o_wn), *h = (float *)(ws + o_h), *tmp = (float *)(ws + o_t);
+    const float *x = fptr(input);
+
+    hipError_t e;
+    {
+        KScope ks("router_logits");
+        e = launch_gemv(router_type, x, n_embd, cptr(w_gate_inp), router_row_stride, fptr(gate_logits), n_expert, 1,
+                        (int)n_expert, (int)n_embd, wn, g.stream);
+    }
+    if (e != hipSuccess) return report(e, "moe_ffn router");
+    RouteArgs ra{};
+    ra.logits = fptr(gate_logits);
+    ra.logits_out = nullptr;
+    ra.idx = idx;
+    ra.scores = sc;
+    ra.T = 1;
+    ra.E = (int)n_expert;
+    ra.k = (int)n_used;
+    ra.logit_stride = n_expert;
+    ra.out_stride = n_used;
+    ra.norm = norm_topk_prob;
+    ra.x = x;
+    ra.K = (int)n_embd;
+    ra.rtype = router_type;
+    ra.rw = cptr(w_gate_inp);
+    ra.rstride = router_row_stride;
+    ra.wnorm2 = wn;
+    ra.guard_count = g.guard;
+    {
+        KScope ks("router_topk");
+        e = launch_route(ra, g.stream);
+    }
+    if (e != hipSuccess) return report(e, "moe_ffn topk");
+    if (has_shared &&
+        run_shared(x, w_shared_gate, w_shared_up, w_shared_down, shared_gate_type, shared_up_type, shared_down_type,
+                   shared_gate_row_stride, shared_up_row_stride, shared_down_row_stride, n_embd, n_ff_shared,
+                   fptr(output), h, tmp) != 0)
+        return -1;
+    ExpertWeights ew = make_ew(w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type, down_type, gate_row_stride,
+                               up_row_stride, down_row_stride, expert_offsets);
+    if (run_experts_decode(x, n_embd, idx, sc, 1, (int)n_used, ew, n_embd, n_ff_exp, fptr(output), nullptr, true, h,
+                           tmp) != 0)
+        return -1;
+    return finish(hipSuccess, "moe_ffn");
+}
+
+extern "C" int ds3_hip_moe_ffn_router(const ds3_hip_buffer_t *input, const ds3_hip_buffer_t *w_gate_inp,
+                                      ds3_hip_buffer_t *gate_logits, uint32_t n_embd, uint32_t n_expert,
+                                      uint64_t router_row_stride, ds3_hip_type_t router_type)
+{
+    if (router_type == T_F32)
+        return ds3_hip_vec_matmul_f32(input, w_gate_inp, gate_logits, n_embd, n_expert, router_row_stride);
+    return ds3_hip_vec_matmul_quantized(input, w_gate_inp, gate_logits, n_embd, n_expert, router_row_stride,
+                                        router_type);
+}
+
+// reference src/ds3_metal.m:2172-2290
+extern "C" int ds3_hip_moe_ffn_experts(
+    const ds3_hip_buffer_t *input, const ds3_hip_buffer_t *w_gate_exps, const ds3_hip_buffer_t *w_up_exps,
+    const ds3_hip_buffer_t *w_down_exps, ds3_hip_type_t gate_type, ds3_hip_type_t up_type, ds3_hip_type_t down_type,
+    uint64_t gate_row_stride, uint64_t up_row_stride, uint64_t down_row_stride, const ds3_hip_buffer_t *w_shared_gate,
+    const ds3_hip_buffer_t *w_shared_up, const ds3_hip_buffer_t *w_shared_down, ds3_hip_type_t shared_gate_type,
+    ds3_hip_type_t shared_up_type, ds3_hip_type_t shared_down_type, uint64_t shared_gate_row_stride,
+    uint64_t shared_up_row_stride, uint64_t shared_down_row_stride, ds3_hip_buffer_t *output, ds3_hip_buffer_t *hidden,
+    ds3_hip_buffer_t *expert_up, ds3_hip_buffer_t *expert_down, uint32_t n_embd, uint32_t n_used, uint32_t n_ff_exp,
+    uint32_t n_ff_shared, const int32_t *indices_host, const float *scores_host)
+{
+    (void)hidden;
+    (void)expert_up;
+    (void)expert_down;
+    if (!input || !w_gate_exps || !w_up_exps || !w_down_exps || !output || !indices_host || !scores_host) return -1;
+    if (n_embd == 0 || n_used == 0 || n_ff_exp == 0) return -1;
+    const bool has_shared = w_shared_gate && w_shared_up && w_shared_down;
+    if (!quant_type_ok_for_moe(gate_type, n_embd, "gate") || !quant_type_ok_for_moe(up_type, n_embd, "up") ||
+        !quant_type_ok_for_moe(down_type, n_ff_exp, "down"))
+        return -1;
+    if (has_shared && (!quant_type_ok_for_moe(shared_gate_type, n_embd, "shared_gate") ||
+                       !quant_type_ok_for_moe(shared_up_type, n_embd, "shared_up") ||
+                       !quant_type_ok_for_moe(shared_down_type, n_ff_shared, "shared_down")))
+        return -1;
+    if (n_used > 16 || !ensure_init()) return -1;
+    // Host-selected expert ids must address rows inside every expert tensor.
+    {
+        const uint64_t ne_g = gate_row_stride ? w_gate_exps->bytes / ((uint64_t)n_ff_exp * gate_row_stride) : 0;
+        const uint64_t ne_u = up_row_stride ? w_up_exps->bytes / ((uint64_t)n_ff_exp * up_row_stride) : 0;
+        const uint64_t ne_d = down_row_stride ? w_down_exps->bytes / ((uint64_t)n_embd * down_row_stride) : 0;
+        const uint64_t ne = ne_g < ne_u ? (ne_g < ne_d ? ne_g : ne_d) : (ne_u < ne_d ? ne_u : ne_d);
+        for (uint32_t i = 0; i < n_used; i++) {
+            if (indices_host[i] < 0 || (uint64_t)indices_host[i] >= ne) {
+                fprintf(stderr, "ds3_hip: moe_ffn_experts: expert id %d outside the %llu experts the weights hold\n",
+                        indices_host[i], (unsigned long long)ne);
+                return -1;
+            }
+        }
+    }
+    const uint32_t ff_max = has_shared && n_ff_shared > n_ff_exp ? n_ff_shared : n_ff_exp;
+    Bump bp;
+    const size_t o_idx = bp.take((size_t)n_used * 4), o_sc = bp.take((size_t)n_used * 4);
+    const size_t o_h = bp.take((size_t)n_used * ff_max * 4), o_t = bp.take((size_t)n_used * ff_max * 4);
+    uint8_t *ws = ws_get(bp.off);
+    if (!ws) return -1;
+    int32_t *idx = (int32_t *)(ws + o_idx);
+    float *sc = (float *)(ws + o_sc), *h = (float *)(ws + o_h), *tmp = (float *)(ws + o_t);
+    if (hipMemcpyAsync(idx, indices_host, (size_t)n_used * 4, hipMemcpyHostToDevice, g.stream) != hipSuccess ||
+        hipMemcpyAsync(sc, scores_host, (size_t)n_used * 4, hipMemcpyHostToDevice, g.stream) != hipSuccess)
+        return -1;
+    const float *x = fptr(input);
+    if (has_shared &&
+        run_shared(x, w_shared_gate, w_shared_up, w_shared_down, shared_gate_type, shared_up_type, shared_down_type,
+                   shared_gate_row_stride, shared_up_row_stride, shared_down_row_stride, n_embd, n_ff_shared,
+                   fptr(output), h, tmp) != 0)
+        return -1;
+    ExpertWeights ew = make_ew(w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type, down_type, gate_row_stride,
+                               up_row_stride, down_row_stride, nullptr);
+    if (run_experts_decode(x, n_embd, idx, sc, 1, (int)n_used, ew, n_embd, n_ff_exp, fptr(output), nullptr, true, h,
+                           tmp) != 0)
+        return -1;
+    return finish(hipSuccess, "moe_ffn_experts");
+}
+
+static int topk_rows(const ds3_hip_buffer_t *logits, ds3_hip_buffer_t *indices, ds3_hip_buffer_t *scores, uint32_t rows,
+                     uint32_t n_expert, uint32_t n_used, bool norm, const char *what)
+{
+    if (!logits || !indices || !scores || rows == 0 || n_expert == 0 || n_used == 0) return -1;
+    if (n_used > n_expert || n_expert > 256 || n_used > 32 || !ensure_init()) return -1;
+    if (!fits(logits, (size_t)rows * n_expert * 4, "logits") || !fits(indices, (size_t)rows * n_used * 4, "indices") ||
+        !fits(scores, (size_t)rows * n_used * 4, "scores"))
+        return -1;
+    RouteArgs ra{};
+    ra.logits = fptr(logits);
+    ra.idx = (int32_t *)dptr(indices);
+    ra.scores = fptr(scores);
+    ra.T = (int)rows;
+    ra.E = (int)n_expert;
+    ra.k = (int)n_used;
+    ra.logit_stride = n_expert;
+    ra.out_stride = n_used;
+    ra.norm = norm;
+    KScope ks("router_topk");
+    return finish(launch_route(ra, g.stream), what);
+}
+
+extern "C" int ds3_hip_moe_router_topk_batch(const ds3_hip_buffer_t *logits, ds3_hip_buffer_t *indices,
+                                             ds3_hip_buffer_t *scores, uint32_t n_layers, uint32_t n_expert,
+                                             uint32_t n_used, bool norm_topk_prob)
+{
+    return topk_rows(logits, indices, scores, n_layers, n_expert, n_used, norm_topk_prob, "moe_router_topk_batch");
+}
+
+extern "C" int ds3_hip_moe_router_topk_batch_tokens(const ds3_hip_buffer_t *logits, ds3_hip_buffer_t *indices,
+                                                    ds3_hip_buffer_t *scores, uint32_t n_layers, uint32_t n_tokens,
+                                                    uint32_t n_expert, uint32_t n_used, bool norm_topk_prob)
+{
+    if (n_tokens == 0) return -1;
+    return topk_rows(logits, indices, scores, n_layers * n_tokens, n_expert, n_used, norm_topk_prob,
+                     "moe_router_topk_batch_tokens");
+}
+
+// ===========================================================================
+// Device-routed extensions
+// ===========================================================================
+
+namespace {
+
+struct RouteBufs {
+    float *logits;
+    int32_t *idx;
+    float *scores;
+    float *wnorm2;
+};
+
+int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstride, int rtype, int T, uint32_t n_embd,
+                 uint32_t n_expert, uint32_t n_used, bool norm, const RouteBufs &rb)
+{
+    hipError_t e;
+    {
+        KScope ks("router_logits");
+        e = launch_gemv(rtype, x, n_embd, cptr(router), rstride, rb.logits, n_expert, T, (int)n_expert, (int)n_embd,
+                        rb.wnorm2, g.stream);
+    }
+    if (e != hipSuccess) return report(e, "router logits");
+    RouteArgs ra{};
+    ra.logits = rb.logits;
+    ra.logits_out = nullptr;
+    ra.idx = rb.idx;
+    ra.scores = rb.scores;
+    ra.T = T;
+    ra.E = (int)n_expert;
+    ra.k = (int)n_used;
+    ra.logit_stride = n_expert;
+    ra.out_stride = n_used;
+    ra.norm = norm;
+    ra.x = x;
+    ra.K = (int)n_embd;
+    ra.rtype = rtype;
+    ra.rw = cptr(router);
+    ra.rstride = rstride;
+    ra.wnorm2 = rb.wnorm2;
+    ra.guard_count = g.guard;
+    KScope ks("router_topk");
+    return report(launch_route(ra, g.stream), "router topk");
+}
+
+// Largest token chunk whose bucketing bitmaps fit in LDS.
+int prefill_chunk(uint32_t n_expert)
+{
+    int c = (int)(61440 / (6 * n_expert)) * 32;
+    if (c > 2048) c = 2048;
+    if (c < 32) c = 32;
+    return c;
+}
+
+}  // namespace
+
+extern "C" int ds3_hip_moe_route(const ds3_hip_buffer_t *input, const ds3_hip_buffer_t *w_gate_inp,
+                                 ds3_hip_buffer_t *gate_logits, ds3_hip_buffer_t *indices, ds3_hip_buffer_t *scores,
+                                 uint32_t n_tokens, uint32_t n_embd, uint32_t n_expert, uint32_t n_used,
+                                 uint64_t router_row_stride, ds3_hip_type_t router_type, bool norm_topk_prob)
+{
+    if (!input || !w_gate_inp || !indices || !scores || n_tokens == 0 || n_embd == 0 || n_expert == 0 ||
+        n_used == 0 || n_used > n_expert || !ensure_init())
+        return -1;
+    if (!moe_limits_ok(n_expert, n_used) || !gemv_type_ok(router_type, (int)n_embd)) return -1;
+    const size_t T = n_tokens;
+    if (!fits(input, T * n_embd * 4, "input") || !fits(indices, T * n_used * 4, "indices") ||
+        !fits(scores, T * n_used * 4, "scores") || !fits(gate_logits, T * n_expert * 4, "gate_logits"))
+        return -1;
+    Bump bp;
+    const size_t o_l = bp.take(T * n_expert * 4), o_w = bp.take((size_t)n_expert * 4);
+    uint8_t *ws = ws_get(bp.off);
+    if (!ws) return -1;
+    RouteBufs rb{ gate_logits ? fptr(gate_logits) : (float *)(ws + o_l), (int32_t *)dptr(indices), fptr(scores),
+                  (float *)(ws + o_w) };
+    if (route_tokens(fptr(input), w_gate_inp, router_row_stride, router_type, (int)T, n_embd, n_expert, n_used,
+                     norm_topk_prob, rb) != 0)
+        return -1;
+    return finish(hipSuccess, "moe_route");
+}
+
+extern "C" int ds3_hip_moe_bucket(const ds3_hip_buffer_t *indices, const ds3_hip_buffer_t *scores, uint32_t n_tokens,
+                                  uint32_t n_used, uint32_t n_expert, ds3_hip_buffer_t *counts,
+                                  ds3_hip_buffer_t *offsets, ds3_hip_buffer_t *ids, ds3_hip_buffer_t *wts,
+                                  ds3_hip_buffer_t *slot_pos)
+{
+    if (!indices || !scores || !counts || !offsets || !ids || !wts || !slot_pos || n_tokens == 0 || n_used == 0 ||
+        n_expert == 0 || !ensure_init())
+        return -1;
+    const size_t S = (size_t)n_tokens * n_used;
+    if (!fits(indices, S * 4, "indices") || !fits(scores, S * 4, "scores") || !fits(counts, n_expert * 4, "counts") ||
+        !fits(offsets, ((size_t)n_expert + 1) * 4, "offsets") || !fits(ids, S * 4, "ids") ||
+        !fits(wts, S * 4, "wts") || !fits(slot_pos, S * 4, "slot_pos"))
+        return -1;
+    const int max_tiles = (int)((S + 63) / 64) + (int)n_expert;
+    Bump bp;
+    const size_t o_t = bp.take((size_t)max_tiles * 4), o_n = bp.take(4);
+    uint8_t *ws = ws_get(bp.off);
+    if (!ws) return -1;
+    BucketOut bo{ (int32_t *)dptr(counts), (int32_t *)dptr(offsets), (int32_t *)dptr(ids), fptr(wts),
+                  (int32_t *)dptr(slot_pos), (int32_t *)(ws + o_t), (int32_t *)(ws + o_n), max_tiles, 64 };
+    KScope ks("bucket");
+    return finish(launch_bucket((const int32_t *)dptr(indices), fptr(scores), (int)n_tokens, (int)n_used,
+                                (int)n_expert, bo, g.stream),
+                  "moe_bucket");
+}
+
+extern "C" int ds3_hip_moe_ffn_batch(
+    const ds3_hip_buffer_t *input, const ds3_hip_buffer_t *w_gate_inp, const ds3_hip_buffer_t *w_gate_exps,
+    const ds3_hip_buffer_t *w_up_exps, const ds3_hip_buffer_t *w_down_exps, ds3_hip_type_t gate_type,
+    ds3_hip_type_t up_type, ds3_hip_type_t down_type, uint64_t gate_row_stride, uint64_t up_row_stride,
+    uint64_t down_row_stride, const ds3_hip_buffer_t *expert_offsets, ds3_hip_buffer_t *output,
+    const ds3_hip_buffer_t *residual, ds3_hip_buffer_t *gate_logits, ds3_hip_buffer_t *indices,
+    ds3_hip_buffer_t *scores, uint32_t n_tokens, uint32_t n_embd, uint32_t n_expert, uint32_t n_used,
+    uint32_t n_ff_exp, uint64_t router_row_stride, ds3_hip_type_t router_type, bool norm_topk_prob)
+{
+    if (!input || !w_gate_inp || !w_gate_exps || !w_up_exps || !w_down_exps || !output) return -1;
+    if (n_tokens == 0 || n_embd == 0 || n_expert == 0 || n_used == 0 || n_ff_exp == 0 || n_used > n_expert)
+        return -1;
+    if (!quant_type_ok_for_moe(gate_type, n_embd, "gate") || !quant_type_ok_for_moe(up_type, n_embd, "up") ||
+        !quant_type_ok_for_moe(down_type, n_ff_exp, "down"))
+        return -1;
+    if (!moe_limits_ok(n_expert, n_used) || !ensure_init()) return -1;
+    if (!gemv_type_ok(router_type, (int)n_embd)) {
+        fprintf(stderr, "ds3_hip: router type %d with n_embd=%u unsupported\n", router_type, n_embd);
+        return -1;
+    }
+    const size_t T = n_tokens;
+    if (!fits(input, T * n_embd * 4, "input") || !fits(output, T * n_embd * 4, "output") ||
+        !fits(residual, T * n_embd * 4, "residual") || !fits(gate_logits, T * n_expert * 4, "gate_logits") ||
+        !fits(indices, T * n_used * 4, "indices") || !fits(scores, T * n_used * 4, "scores"))
+        return -1;
+
+    const bool grouped_ok = gate_type == up_type && grouped_type_ok(gate_type, (int)n_embd) &&
+                            grouped_type_ok(down_type, (int)n_ff_exp) && n_ff_exp % 128 == 0 && n_embd % 128 == 0;
+    const bool use_grouped = grouped_ok && (int)n_tokens >= g.prefill_min;
+    const int chunk = use_grouped ? prefill_chunk(n_expert) : (int)n_tokens;
+    const size_t Tc = (size_t)(chunk < (int)n_tokens ? chunk : (int)n_tokens);
+    const size_t S = Tc * n_used;
+    const int max_tiles = (int)((S + 63) / 64) + (int)n_expert;
+
+    Bump bp;
+    const size_t o_l = bp.take(T * n_expert * 4), o_i = bp.take(T * n_used * 4), o_s = bp.take(T * n_used * 4);
+    const size_t o_w = bp.take((size_t)n_expert * 4);
+    size_t o_h = 0, o_t = 0, o_x16 = 0, o_cnt = 0, o_off = 0, o_ids = 0, o_wts = 0, o_pos = 0, o_tiles = 0, o_nt = 0,
+           o_h16 = 0, o_y = 0;
+    if (use_grouped) {
+        o_x16 = bp.take(Tc * n_embd * 2);
+        o_cnt = bp.take((size_t)n_expert * 4);
+        o_off = bp.take(((size_t)n_expert + 1) * 4);
+        o_ids = bp.take(S * 4);
+        o_wts = bp.take(S * 4);
+        o_pos = bp.take(S * 4);
+        o_tiles = bp.take((size_t)max_tiles * 4);
+        o_nt = bp.take(4);
+        o_h16 = bp.take(S * n_ff_exp * 2);
+        o_y = bp.take(S * n_embd * 4);
+    } else {
+        o_h = bp.take(T * n_used * n_ff_exp * 4);
+        o_t = bp.take(T * n_used * n_ff_exp * 4);
+    }
+    uint8_t *ws = ws_get(bp.off);
+    if (!ws) return -1;
+    RouteBufs rb{ gate_logits ? fptr(gate_logits) : (float *)(ws + o_l),
+                  indices ? (int32_t *)dptr(indices) : (int32_t *)(ws + o_i),
+                  scores ? fptr(scores) : (float *)(ws + o_s), (float *)(ws + o_w) };
+    const float *x = fptr(input);
+    if (route_tokens(x, w_gate_inp, router_row_stride, router_type, (int)T, n_embd, n_expert, n_used, norm_topk_prob,
+                     rb) != 0)
+        return -1;
+    ExpertWeights ew = make_ew(w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type, down_type, gate_row_stride,
+                               up_row_stride, down_row_stride, expert_offsets);
+    float *out = fptr(output);
+    const float *res = residual ? fptr(residual) : nullptr;
+    if (!use_grouped) {
+        if (run_experts_decode(x, n_embd, rb.idx, rb.scores, (int)T, (int)n_used, ew, n_embd, n_ff_exp, out, res, true,
+                               (float *)(ws + o_h), (float *)(ws + o_t)) != 0)
+            return -1;
+        return finish(hipSuccess, "moe_ffn_batch");
+    }
+    BucketOut bo{ (int32_t *)(ws + o_cnt), (int32_t *)(ws + o_off), (int32_t *)(ws + o_ids), (float *)(ws + o_wts),
+                  (int32_t *)(ws + o_pos), (int32_t *)(ws + o_tiles), (int32_t *)(ws + o_nt), max_tiles, 64 };
+    _Float16 *x16 = (_Float16 *)(ws + o_x16), *h16 = (_Float16 *)(ws + o_h16);
+    float *y = (float *)(ws + o_y);
+    for (size_t t0 = 0; t0 < T; t0 += Tc) {
+        const int tc = (int)((T - t0) < Tc ? (T - t0) : Tc);
+        const float *xc = x + t0 * n_embd;
+        hipError_t e;
+        {
+            KScope ks("to_f16");
+            e = launch_to_f16(xc, x16, (int64_t)tc * n_embd, g.stream);
+        }
+        if (e == hipSuccess) {
+            KScope ks("bucket");
+            e = launch_bucket(rb.idx + t0 * n_used, rb.scores + t0 * n_used, tc, (int)n_used, (int)n_expert, bo,
+                              g.stream);
+        }
+        if (e == hipSuccess) {
+            KScope ks("moe_grouped_gate_up");
+            e = launch_grouped_gate_up(x16, (int)n_embd, ew, (int)n_ff_exp, bo, h16, g.stream);
+        }
+        if (e == hipSuccess) {
+            KScope ks("moe_grouped_down");
+            e = launch_grouped_down(h16, (int)n_ff_exp, ew, (int)n_embd, bo, y, g.stream);
+        }
+        if (e == hipSuccess) {
+            KScope ks("moe_combine");
+            e = launch_combine(y, bo.slot_pos, rb.scores + t0 * n_used, tc, (int)n_used, (int)n_embd,
+                               out + t0 * n_embd, n_embd, res ? res + t0 * n_embd : nullptr, true, g.stream);
+        }
+        if (e != hipSuccess) return report(e, "moe_ffn_batch grouped");
+    }
+    return finish(hipSuccess, "moe_ffn_batch");
+}
+
+extern "C" int ds3_hip_dequantize(const ds3_hip_buffer_t *src, uint64_t src_offset, ds3_hip_type_t type, uint64_t n,
+                                  ds3_hip_buffer_t *dst)
+{
+    if (!src || !dst || n == 0 || !ensure_init()) return -1;
+    int64_t blk = 0, bytes = 0;
+    switch (type) {
+    case T_F32: blk = 1; bytes = 4; break;
+    case T_F16: blk = 1; bytes = 2; break;
+    case T_Q8_0: blk = 32; bytes = 34; break;
+    case T_Q4_K: blk = 256; bytes = 144; break;
+    case T_Q6_K: blk = 256; bytes = 210; break;
+    default: fprintf(stderr, "ds3_hip: dequantize: unsupported type %d\n", type); return -1;
+    }
+    if (n % (uint64_t)blk != 0) {
+        fprintf(stderr, "ds3_hip: dequantize: n=%llu not a multiple of %lld\n", (unsigned long long)n, (long long)blk);
+        return -1;
+    }
+    if ((type == T_Q6_K || type == T_Q8_0 || type == T_F16) && (src_offset & 1)) return -1;
+    if ((type == T_Q4_K) && (src_offset & 15)) {
+        fprintf(stderr, "ds3_hip: dequantize: Q4_K source offset must be 16-byte aligned\n");
+        return -1;
+    }
+    if (type == T_F32 && (src_offset & 3)) return -1;
+    if (!fits(src, src_offset + n / blk * bytes, "src") || !fits(dst, n * 4, "dst")) return -1;
+    KScope ks("dequant");
+    return finish(launch_dequant(type, cptr(src) + src_offset, fptr(dst), (int64_t)n, g.stream), "dequantize");
+}
+
+extern "C" int ds3_hip_set_prefill_min_tokens(int min_tokens)
+{
+    const int prev = g.prefill_min;
+    g.prefill_min = min_tokens > 0 ? min_tokens : kDefaultPrefillMin;
+    return prev;
+}
+
+extern "C" int64_t ds3_hip_guard_count(void)
+{
+    if (!g.inited) return 0;
+    int32_t v = 0;
+    (void)hipStreamSynchronize(g.stream);
+    (void)hipMemcpy(&v, g.guard, sizeof v, hipMemcpyDeviceToHost);
+    return v;
+}
+
+// ===========================================================================
+// Batching and profiling (reference src/ds3_metal.m:2830-2900)
+// ===========================================================================
+
+extern "C" int ds3_hip_begin_batch(void)
+{
+    if (!ensure_init()) return -1;
+    if (g.batch) {
+        fprintf(stderr, "ds3_hip: begin_batch called while already in batch mode\n");
+        return -1;
+    }
+    g.batch = true;
+    if (g.profile) (void)hipEventRecord(g.bev0, g.stream);
+    return 0;
+}
+
+extern "C" void ds3_hip_end_batch(void)
+{
+    if (!g.batch) return;
+    if (g.profile) (void)hipEventRecord(g.bev1, g.stream);
+    const auto c0 = std::chrono::steady_clock::now();
+    (void)hipStreamSynchronize(g.stream);
+    const auto c1 = std::chrono::steady_clock::now();
+    if (g.profile) {
+        float ms = 0.f;
+        (void)hipEventElapsedTime(&ms, g.bev0, g.bev1);
+        g.gpu_ms += ms;
+        g.cpu_ms += std::chrono::duration<double, std::milli>(c1 - c0).count();
+        g.cb_count++;
+    }
+    g.batch = false;
+}
+
+extern "C" void ds3_hip_synchronize(void)
+{
+    if (g.inited) (void)hipStreamSynchronize(g.stream);
+}
+
+extern "C" void ds3_hip_profile_reset(void)
+{
+    g.cb_count = 0;
+    g.gpu_ms = 0.0;
+    g.cpu_ms = 0.0;
+}
+
+extern "C" void ds3_hip_profile_print(const char *label)
+{
+    if (!g.profile) return;
+    fprintf(stderr, "[profile %s] cb_count=%d total_gpu_ms=%.3f total_cpu_wait_ms=%.3f\n", label ? label : "",
+            g.cb_count, g.gpu_ms, g.cpu_ms);
+}
+
+extern "C" void ds3_hip_kernel_timing(int enable)
+{
+    if (!ensure_init()) return;
+    if (enable && g.pool.empty()) {
+        g.pool.resize(16384);
+        for (auto &e : g.pool) (void)hipEventCreate(&e);
+    }
+    g.ktiming = enable != 0;
+}
+
+extern "C" void ds3_hip_kernel_timing_reset(void)
+{
+    if (g.inited) (void)hipStreamSynchronize(g.stream);
+    g.recs.clear();
+    g.pool_used = 0;
+    g.stat_names.clear();
+    g.stat_count.clear();
+    g.stat_ms.clear();
+    g.stats_dirty = true;
+}
+
+extern "C" int ds3_hip_kernel_stats(int i, char *name, size_t name_len, int64_t *count, double *total_ms)
+{
+    if (!g.inited) return -1;
+    if (g.stats_dirty) {
+        (void)hipStreamSynchronize(g.stream);
+        g.stat_names.clear();
+        g.stat_count.clear();
+        g.stat_ms.clear();
+        for (const KRec &r : g.recs) {
+            float ms = 0.f;
+            (void)hipEventElapsedTime(&ms, g.pool[r.e0], g.pool[r.e1]);
+            size_t j = 0;
+            while (j < g.stat_names.size() && g.stat_names[j] != r.name) j++;
+            if (j == g.stat_names.size()) {
+                g.stat_names.emplace_back(r.name);
+                g.stat_count.push_back(0);
+                g.stat_ms.push_back(0.0);
+            }
+            g.stat_count[j]++;
+            g.stat_ms[j] += ms;
+        }
+        g.stats_dirty = false;
+    }
+    if (i < 0 || i >= (int)g.stat_names.size()) return -1;
+    if (name && name_len) {
+        strncpy(name, g.stat_names[i].c_str(), name_len - 1);
+        name[name_len - 1] = 0;
+    }
+    if (count) *count = g.stat_count[i];
+    if (total_ms) *total_ms = g.stat_ms[i];
+    return 0;
+}
+
+extern "C" int ds3_hip_timer_start(void)
+{
+    if (!ensure_init()) return -1;
+    return report(hipEventRecord(g.t0, g.stream), "timer_start");
+}
+
+extern "C" double ds3_hip_timer_stop_ms(void)
+{
+    if (!g.inited) return -1.0;
+    (void)hipEventRecord(g.t1, g.stream);
+    (void)hipEventSynchronize(g.t1);
+    float ms = 0.f;
+    (void)hipEventElapsedTime(&ms, g.t0, g.t1);
+    return ms;
+}
+
+extern "C" int ds3_hip_device_info(char *arch, size_t arch_len, int *n_cu, uint64_t *hbm_bytes)
+{
+    if (!ensure_init()) return -1;
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, 0) != hipSuccess) return -1;
+    if (arch && arch_len) {
+        strncpy(arch, p.gcnArchName, arch_len - 1);
+        arch[arch_len - 1] = 0;
+    }
+    if (n_cu) *n_cu = p.multiProcessorCount;
+    if (hbm_bytes) *hbm_bytes = p.totalGlobalMem;
+    return 0;
+}

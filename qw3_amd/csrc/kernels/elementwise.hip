@@ -1,0 +1,163 @@
+// elementwise.hip -- small memory-bound kernels around the expert products.
+//
+// gather / scatter / silu_mul / add / copy / zero keep the reference's
+// elementwise entry points (metal/elementwise.metal:7-88, metal/moe.metal:95-127);
+// combine is the deterministic per-token reduction of the prefill path: each
+// output element sums its k routed contributions in top-k order
+// (reference src/ds3_reference.c:674-678), so no float atomics are needed.
+#include "common.h"
+#include "launch.h"
+
+namespace ds3k {
+
+constexpr int EW_TPB = 256;
+
+static dim3 grid1d(int64_t n) { return dim3((unsigned)((n + EW_TPB - 1) / EW_TPB)); }
+
+__global__ void k_fill_zero(float *p, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * EW_TPB + threadIdx.x;
+    if (i < n) p[i] = 0.0f;
+}
+
+__global__ void k_copy(const float *a, float *b, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * EW_TPB + threadIdx.x;
+    if (i < n) b[i] = a[i];
+}
+
+__global__ void k_add(const float *a, const float *b, float *c, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * EW_TPB + threadIdx.x;
+    if (i < n) c[i] = a[i] + b[i];
+}
+
+// Row ids outside [0, n_rows) (n_rows from the buffer size) are skipped.
+__global__ void k_gather_rows(const float *src, const int32_t *ids, float *dst, int n_cols, int count, int64_t n_rows)
+{
+    const int64_t i = (int64_t)blockIdx.x * EW_TPB + threadIdx.x;
+    if (i >= (int64_t)n_cols * count) return;
+    const int r = (int)(i / n_cols), c = (int)(i - (int64_t)r * n_cols);
+    const int64_t row = ids[r];
+    if (row >= 0 && row < n_rows) dst[i] = src[row * n_cols + c];
+}
+
+// dst[ids[i]][j] += scores[i] * src[i][j].  Rows of one call must be distinct
+// (the reference's contract: one expert's token list), so there are no races.
+__global__ void k_scatter_add(const float *src, const float *scores, const int32_t *ids, float *dst, int n_cols,
+                              int count, int64_t n_rows)
+{
+    const int64_t i = (int64_t)blockIdx.x * EW_TPB + threadIdx.x;
+    if (i >= (int64_t)n_cols * count) return;
+    const int r = (int)(i / n_cols), c = (int)(i - (int64_t)r * n_cols);
+    const int64_t row = ids[r];
+    if (row < 0 || row >= n_rows) return;
+    float *d = dst + row * n_cols + c;
+    *d = *d + scores[r] * src[i];
+}
+
+__global__ void k_silu_mul(const float *g, const float *u, float *out, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * EW_TPB + threadIdx.x;
+    if (i < n) out[i] = swiglu(g[i], u[i]);
+}
+
+__global__ void k_axpy(const float *x, float w, float *y, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * EW_TPB + threadIdx.x;
+    if (i < n) y[i] = y[i] + w * x[i];
+}
+
+__global__ void k_to_f16(const float *x, _Float16 *y, int64_t n4)
+{
+    const int64_t i = (int64_t)blockIdx.x * EW_TPB + threadIdx.x;
+    if (i >= n4) return;
+    const float4 v = ((const float4 *)x)[i];
+    typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+    half4 h;
+    h[0] = (_Float16)v.x; h[1] = (_Float16)v.y; h[2] = (_Float16)v.z; h[3] = (_Float16)v.w;
+    ((half4 *)y)[i] = h;
+}
+
+// out[t][j] = (acc ? out[t][j] : 0) + w_0 y[p_0][j] + ... in k order, then + residual.
+__global__ void k_combine(const float *__restrict__ y, const int32_t *__restrict__ slot_pos,
+                          const float *__restrict__ wts, int k, int N, float *__restrict__ out, int64_t ldo,
+                          const float *__restrict__ residual, int accumulate)
+{
+#pragma clang fp contract(off)
+    const int t = blockIdx.y;
+    const int j = blockIdx.x * EW_TPB + threadIdx.x;
+    if (j >= N) return;
+    float *o = out + (int64_t)t * ldo + j;
+    float acc = accumulate ? *o : 0.0f;
+    for (int kk = 0; kk < k; kk++) {
+        const int p = slot_pos[t * k + kk];
+        if (p >= 0) acc = acc + wts[t * k + kk] * y[(int64_t)p * N + j];
+    }
+    if (residual) acc = acc + residual[(int64_t)t * ldo + j];
+    *o = acc;
+}
+
+hipError_t launch_fill_zero(float *p, int64_t n, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_fill_zero, grid1d(n), dim3(EW_TPB), 0, s, p, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy(const float *a, float *b, int64_t n, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_copy, grid1d(n), dim3(EW_TPB), 0, s, a, b, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_add(const float *a, const float *b, float *c, int64_t n, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_add, grid1d(n), dim3(EW_TPB), 0, s, a, b, c, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const float *src, const int32_t *ids, float *dst, int n_cols, int count,
+                              int64_t n_rows, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_gather_rows, grid1d((int64_t)n_cols * count), dim3(EW_TPB), 0, s, src, ids, dst, n_cols,
+                       count, n_rows);
+    return hipGetLastError();
+}
+
+hipError_t launch_scatter_add(const float *src, const float *scores, const int32_t *ids, float *dst, int n_cols,
+                              int count, int64_t n_rows, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_scatter_add, grid1d((int64_t)n_cols * count), dim3(EW_TPB), 0, s, src, scores, ids, dst,
+                       n_cols, count, n_rows);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(const float *g, const float *u, float *out, int64_t n, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_silu_mul, grid1d(n), dim3(EW_TPB), 0, s, g, u, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_axpy(const float *x, float w, float *y, int64_t n, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_axpy, grid1d(n), dim3(EW_TPB), 0, s, x, w, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_to_f16(const float *x, _Float16 *y, int64_t n, hipStream_t s)
+{
+    if (n % 4) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_to_f16, grid1d(n / 4), dim3(EW_TPB), 0, s, x, y, n / 4);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine(const float *y, const int32_t *slot_pos, const float *wts, int T, int k, int N, float *out,
+                          int64_t ldo, const float *residual, bool accumulate, hipStream_t s)
+{
+    const dim3 grid((unsigned)((N + EW_TPB - 1) / EW_TPB), (unsigned)T);
+    hipLaunchKernelGGL(k_combine, grid, dim3(EW_TPB), 0, s, y, slot_pos, wts, k, N, out, ldo, residual,
+                       accumulate ? 1 : 0);
+    return hipGetLastError();
+}
+
+}  // namespace ds3k

@@ -1,0 +1,111 @@
+// launch.h -- host-side launchers of the gfx950 kernels (internal interface
+// between the C-ABI layer ds3_hip.cpp and the kernel translation units).
+// Every launcher enqueues on `s` and returns hipGetLastError().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ds3k {
+
+// GGUF type ids (reference src/ds3.h:201-216).
+enum : int { T_F32 = 0, T_F16 = 1, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+
+// Where the three expert matrices of expert e start: either e * rows * stride
+// or, if `table` is non-null, table[3e + {0,1,2}] (gate, up, down) bytes.
+struct ExpertWeights {
+    const uint8_t *gate, *up, *down;    // base of each packed [n_expert][rows][..] tensor
+    uint64_t gate_stride, up_stride, down_stride;   // bytes per row
+    int gate_type, up_type, down_type;
+    const uint64_t *table;              // optional device [n_expert][3] byte offsets
+};
+
+hipError_t launch_dequant(int type, const void *src, float *dst, int64_t n, hipStream_t s);
+
+// C[m][n] = sum_k A[m*lda + k] * W(row n)[k], W rows at w + n*stride, fp32
+// accumulate.  If wnorm2 != nullptr also writes sum_k W[n][k]^2 to wnorm2[n].
+hipError_t launch_gemv(int type, const float *A, int64_t lda, const uint8_t *w, uint64_t stride,
+                       float *C, int64_t ldc, int M, int N, int K, float *wnorm2, hipStream_t s);
+
+bool gemv_type_ok(int type, int K);
+
+// Router tail: logits [T][E] -> softmax -> top-k -> renorm, selected by
+// (prob desc, index asc) like the reference.  If x != nullptr the margin
+// guard recomputes near-tie logits in the reference's sequential order from
+// x [T][K] and router rows (rtype, rw, rstride); wnorm2 [E] must then be set.
+// logits_out (may alias logits) receives the logits actually used.
+struct RouteArgs {
+    const float *logits;
+    float *logits_out;
+    int32_t *idx;
+    float *scores;
+    int T, E, k;
+    int64_t logit_stride;      // floats between tokens' logit rows
+    int64_t out_stride;        // int32/float entries between tokens' idx/scores rows
+    bool norm;
+    const float *x;
+    int K;
+    int rtype;
+    const uint8_t *rw;
+    uint64_t rstride;
+    const float *wnorm2;
+    int32_t *guard_count;      // optional: number of tokens that took the exact recompute
+};
+hipError_t launch_route(const RouteArgs &a, hipStream_t s);
+
+// Decode (small T) expert products.
+//   h[slot][F] = silu(x[t] . Wg_e) * (x[t] . Wu_e), slot = t*n_used + k, e = idx[slot]
+hipError_t launch_decode_gate_up(const float *x, int64_t ldx, const int32_t *idx, int n_slots,
+                                 int n_used, const ExpertWeights &ew, int K, int F,
+                                 float *h, hipStream_t s);
+//   out[slot][F] = x[t] . W_e with W = ew.gate / gate_type / gate_stride and
+//   expert offsets from table column `which` (0 gate, 1 up).
+hipError_t launch_decode_proj(const float *x, int64_t ldx, const int32_t *idx, int n_slots, int n_used,
+                              const ExpertWeights &ew, int which, int K, int F, float *out, hipStream_t s);
+//   out[t][j] (+)= sum_k w[t][k] * (h[slot] . Wd_e[j]) in k order
+hipError_t launch_decode_down(const float *h, const int32_t *idx, const float *wts, int T,
+                              int n_used, const ExpertWeights &ew, int K, int F,
+                              float *out, int64_t ldo, const float *residual, bool accumulate,
+                              hipStream_t s);
+
+// Bucketing of T*n_used slots by expert, token order within each expert.
+struct BucketOut {
+    int32_t *counts;     // [E]
+    int32_t *offsets;    // [E+1]
+    int32_t *ids;        // [T*k] token of each compacted position
+    float *wts;          // [T*k] routing weight of each position
+    int32_t *slot_pos;   // [T*k] position of slot t*k+j
+    int32_t *tiles;      // [max_tiles] packed (expert << 16 | m_tile) work items for the GEMMs
+    int32_t *n_tiles;    // [1]
+    int max_tiles;
+    int tile_m;
+};
+hipError_t launch_bucket(const int32_t *idx, const float *scores, int T, int k, int E,
+                         const BucketOut &o, hipStream_t s);
+
+// Prefill grouped products (fp16 MFMA, fp32 accumulate).
+hipError_t launch_to_f16(const float *x, _Float16 *y, int64_t n, hipStream_t s);
+hipError_t launch_grouped_gate_up(const _Float16 *x16, int K, const ExpertWeights &ew, int F,
+                                  const BucketOut &b, _Float16 *h16, hipStream_t s);
+hipError_t launch_grouped_down(const _Float16 *h16, int F, const ExpertWeights &ew, int N,
+                               const BucketOut &b, float *y, hipStream_t s);
+bool grouped_type_ok(int type, int K);
+
+// out[t][j] = (accumulate ? out : 0) + sum_k w[t][k] * y[slot_pos[t*k+kk]][j] (+ residual)
+hipError_t launch_combine(const float *y, const int32_t *slot_pos, const float *wts, int T, int k,
+                          int N, float *out, int64_t ldo, const float *residual, bool accumulate,
+                          hipStream_t s);
+
+// Elementwise helpers (reference metal/elementwise.metal, metal/moe.metal:95-127).
+hipError_t launch_fill_zero(float *p, int64_t n, hipStream_t s);
+hipError_t launch_copy(const float *a, float *b, int64_t n, hipStream_t s);
+hipError_t launch_add(const float *a, const float *b, float *c, int64_t n, hipStream_t s);
+// Row ids outside [0, n_rows) are skipped.
+hipError_t launch_gather_rows(const float *src, const int32_t *ids, float *dst, int n_cols, int count,
+                              int64_t n_rows, hipStream_t s);
+hipError_t launch_scatter_add(const float *src, const float *scores, const int32_t *ids, float *dst,
+                              int n_cols, int count, int64_t n_rows, hipStream_t s);
+hipError_t launch_silu_mul(const float *g, const float *u, float *out, int64_t n, hipStream_t s);
+hipError_t launch_axpy(const float *x, float w, float *y, int64_t n, hipStream_t s);
+
+}  // namespace ds3k

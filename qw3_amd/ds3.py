@@ -1,0 +1,195 @@
+"""Python host mirror of the ds3_hip C ABI (include/ds3_hip.h).
+
+Thin wrappers that keep the reference's entry-point names and argument
+meaning (reference src/ds3_metal.h) and turn a -1 return into an exception.
+Device memory is owned by ds3_hip buffers; numpy arrays cross the boundary
+through buffer_write / buffer_read.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._native import hip
+
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 8, 12, 14
+TYPE_NAMES = {TYPE_F32: "F32", TYPE_F16: "F16", TYPE_Q8_0: "Q8_0", TYPE_Q4_K: "Q4_K", TYPE_Q6_K: "Q6_K"}
+# (values per block, bytes per block) -- reference src/ds3_reference.c:59-184
+BLOCK = {TYPE_F32: (1, 4), TYPE_F16: (1, 2), TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144), TYPE_Q6_K: (256, 210)}
+
+
+class Ds3Error(RuntimeError):
+    pass
+
+
+def row_bytes(type_: int, n_cols: int) -> int:
+    per, nb = BLOCK[type_]
+    if n_cols % per:
+        raise ValueError(f"{n_cols} columns do not fill {TYPE_NAMES[type_]} blocks")
+    return n_cols // per * nb
+
+
+def init() -> None:
+    if hip().ds3_hip_init() != 0:
+        raise Ds3Error("ds3_hip_init failed (no HIP device?)")
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise Ds3Error(f"{what} returned {rc}")
+
+
+class Buffer:
+    """A ds3_hip_buffer_t handle.  Frees its memory when closed or collected."""
+
+    def __init__(self, handle: int, nbytes: int, owner: bool = True):
+        if not handle:
+            raise Ds3Error("buffer allocation failed")
+        self.handle = C.c_void_p(handle)
+        self.nbytes = nbytes
+        self._owner = owner
+
+    @classmethod
+    def alloc(cls, nbytes: int) -> "Buffer":
+        return cls(hip().ds3_hip_buffer_alloc(nbytes), nbytes)
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "Buffer":
+        a = np.ascontiguousarray(a)
+        b = cls.alloc(max(a.nbytes, 1))
+        b.write(a)
+        return b
+
+    def view(self, offset: int, nbytes: int) -> "Buffer":
+        return Buffer(hip().ds3_hip_buffer_view(self.handle, offset, nbytes), nbytes, owner=True)
+
+    def write(self, a: np.ndarray, offset: int = 0) -> None:
+        a = np.ascontiguousarray(a)
+        _check(hip().ds3_hip_buffer_write(self.handle, offset, a.ctypes.data, a.nbytes), "buffer_write")
+
+    def read(self, dtype, shape, offset: int = 0) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        _check(hip().ds3_hip_buffer_read(self.handle, offset, out.ctypes.data, out.nbytes), "buffer_read")
+        return out
+
+    def zero(self) -> None:
+        _check(hip().ds3_hip_buffer_zero_f32(self.handle, self.nbytes - self.nbytes % 4), "buffer_zero_f32")
+
+    def close(self) -> None:
+        if self._owner and self.handle:
+            hip().ds3_hip_buffer_free(self.handle)
+        self.handle = C.c_void_p(0)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _h(b):
+    return b.handle if b is not None else None
+
+
+@dataclass
+class ExpertTensors:
+    """Packed expert weights of one layer, expert-major like the GGUF tensors
+    ffn_{gate,up,down}_exps (reference src/ds3_engine.c:977-1003)."""
+    gate: Buffer
+    up: Buffer
+    down: Buffer
+    gate_type: int
+    up_type: int
+    down_type: int
+    n_embd: int
+    n_ff: int
+
+    @property
+    def strides(self):
+        return (row_bytes(self.gate_type, self.n_embd), row_bytes(self.up_type, self.n_embd),
+                row_bytes(self.down_type, self.n_ff))
+
+
+def dequantize(src: Buffer, type_: int, n: int, dst: Buffer, src_offset: int = 0) -> None:
+    _check(hip().ds3_hip_dequantize(src.handle, src_offset, type_, n, dst.handle), "dequantize")
+
+
+def moe_route(x: Buffer, router: Buffer, router_type: int, n_tokens: int, n_embd: int, n_expert: int,
+              n_used: int, indices: Buffer, scores: Buffer, logits: Buffer | None = None,
+              norm: bool = True) -> None:
+    _check(hip().ds3_hip_moe_route(x.handle, router.handle, _h(logits), indices.handle, scores.handle,
+                                   n_tokens, n_embd, n_expert, n_used, row_bytes(router_type, n_embd),
+                                   router_type, norm), "moe_route")
+
+
+def moe_bucket(indices: Buffer, scores: Buffer, n_tokens: int, n_used: int, n_expert: int,
+               counts: Buffer, offsets: Buffer, ids: Buffer, wts: Buffer, slot_pos: Buffer) -> None:
+    _check(hip().ds3_hip_moe_bucket(indices.handle, scores.handle, n_tokens, n_used, n_expert, counts.handle,
+                                    offsets.handle, ids.handle, wts.handle, slot_pos.handle), "moe_bucket")
+
+
+def moe_ffn_batch(x: Buffer, router: Buffer, router_type: int, ex: ExpertTensors, out: Buffer, n_tokens: int,
+                  n_expert: int, n_used: int, residual: Buffer | None = None, logits: Buffer | None = None,
+                  indices: Buffer | None = None, scores: Buffer | None = None, norm: bool = True,
+                  expert_offsets: Buffer | None = None) -> None:
+    gs, us, ds = ex.strides
+    _check(hip().ds3_hip_moe_ffn_batch(
+        x.handle, router.handle, ex.gate.handle, ex.up.handle, ex.down.handle,
+        ex.gate_type, ex.up_type, ex.down_type, gs, us, ds, _h(expert_offsets),
+        out.handle, _h(residual), _h(logits), _h(indices), _h(scores),
+        n_tokens, ex.n_embd, n_expert, n_used, ex.n_ff, row_bytes(router_type, ex.n_embd), router_type, norm),
+        "moe_ffn_batch")
+
+
+def moe_ffn(x: Buffer, router: Buffer, router_type: int, ex: ExpertTensors, out: Buffer, logits: Buffer,
+            n_expert: int, n_used: int, norm: bool = True, scratch: Buffer | None = None,
+            shared: ExpertTensors | None = None, n_ff_shared: int = 0, expert_offsets: Buffer | None = None) -> None:
+    """ds3_metal_moe_ffn-compatible single-token call (reference src/ds3_metal.h:340-374)."""
+    gs, us, ds = ex.strides
+    scratch = scratch or Buffer.alloc(4 * max(ex.n_ff, ex.n_embd, n_ff_shared, 1))
+    if shared is not None:
+        sg, su, sd = shared.gate.handle, shared.up.handle, shared.down.handle
+        sgt, sut, sdt = shared.gate_type, shared.up_type, shared.down_type
+        sgs, sus = row_bytes(sgt, ex.n_embd), row_bytes(sut, ex.n_embd)
+        sds = row_bytes(sdt, n_ff_shared)
+    else:
+        sg = su = sd = None
+        sgt = sut = sdt = TYPE_F32
+        sgs = sus = sds = 0
+    _check(hip().ds3_hip_moe_ffn(
+        x.handle, router.handle, ex.gate.handle, ex.up.handle, ex.down.handle,
+        ex.gate_type, ex.up_type, ex.down_type, gs, us, ds,
+        sg, su, sd, sgt, sut, sdt, sgs, sus, sds,
+        out.handle, logits.handle, _h(expert_offsets), scratch.handle, scratch.handle, scratch.handle,
+        ex.n_embd, n_expert, n_used, ex.n_ff, n_ff_shared, row_bytes(router_type, ex.n_embd), router_type, norm),
+        "moe_ffn")
+
+
+def set_prefill_min_tokens(n: int) -> int:
+    return hip().ds3_hip_set_prefill_min_tokens(n)
+
+
+def guard_count() -> int:
+    return hip().ds3_hip_guard_count()
+
+
+def device_info() -> dict:
+    arch = C.create_string_buffer(64)
+    ncu = C.c_int()
+    hbm = C.c_uint64()
+    _check(hip().ds3_hip_device_info(arch, 64, C.byref(ncu), C.byref(hbm)), "device_info")
+    return {"arch": arch.value.decode(), "n_cu": ncu.value, "hbm_bytes": hbm.value}
+
+
+def kernel_stats() -> dict[str, tuple[int, float]]:
+    """{kernel: (launches, total_ms)} recorded while kernel timing was on."""
+    out = {}
+    name = C.create_string_buffer(128)
+    cnt, ms = C.c_int64(), C.c_double()
+    i = 0
+    while hip().ds3_hip_kernel_stats(i, name, 128, C.byref(cnt), C.byref(ms)) == 0:
+        out[name.value.decode()] = (cnt.value, ms.value)
+        i += 1
+    return out

@@ -1,0 +1,61 @@
+"""Shared GPU-test cases: a synthetic layer on host and device plus its FP32
+dequantisation (via the oracle) and oracle outputs on the same inputs."""
+from __future__ import annotations
+
+import numpy as np
+
+import _oracle as O
+from qw3_amd import ds3
+from qw3_amd import workload as W
+
+TOL_MAX_ABS = 2e-3      # north-star bar on combined outputs
+TOL_REL_L2 = 1e-3
+
+
+class Case:
+    def __init__(self, spec: W.LayerSpec, seed: int = 1234, layer: int = 0):
+        self.spec = spec
+        self.host = W.make_layer(spec, seed, layer)
+        self.dev = self.host.to_device()
+        E, K, F = spec.n_expert, spec.n_embd, spec.n_ff
+        self.wr = O.dequantize(spec.router_type, self.host.router, E * K).reshape(E, K)
+        self.wg = O.dequantize(spec.gate_type, self.host.gate, E * F * K)
+        self.wu = O.dequantize(spec.up_type, self.host.up, E * F * K)
+        self.wd = O.dequantize(spec.down_type, self.host.down, E * K * F)
+
+    def oracle(self, x: np.ndarray, n_used: int = W.N_USED, norm: bool = True, threads: int = 16):
+        s = self.spec
+        return O.moe_tokens(x, self.wr, self.wg, self.wu, self.wd, s.n_expert, n_used, s.n_ff, threads, norm)
+
+    def gpu_batch(self, x: np.ndarray, n_used: int = W.N_USED, prefill_min: int | None = None,
+                  residual: np.ndarray | None = None, norm: bool = True):
+        s = self.spec
+        T = x.shape[0]
+        xb = ds3.Buffer.from_array(x)
+        out = ds3.Buffer.alloc(T * s.n_embd * 4)
+        idx = ds3.Buffer.alloc(T * n_used * 4)
+        sc = ds3.Buffer.alloc(T * n_used * 4)
+        lg = ds3.Buffer.alloc(T * s.n_expert * 4)
+        rb = ds3.Buffer.from_array(residual) if residual is not None else None
+        prev = ds3.set_prefill_min_tokens(prefill_min) if prefill_min else None
+        try:
+            ds3.moe_ffn_batch(xb, self.dev.router, s.router_type, self.dev.experts, out, T, s.n_expert, n_used,
+                              residual=rb, logits=lg, indices=idx, scores=sc, norm=norm)
+        finally:
+            if prev is not None:
+                ds3.set_prefill_min_tokens(prev)
+        return (out.read(np.float32, (T, s.n_embd)), idx.read(np.int32, (T, n_used)),
+                sc.read(np.float32, (T, n_used)), lg.read(np.float32, (T, s.n_expert)))
+
+
+def assert_close(got: np.ndarray, want: np.ndarray, max_abs: float = TOL_MAX_ABS, rel_l2: float = TOL_REL_L2):
+    err = float(np.abs(got.astype(np.float64) - want).max())
+    rl = O.rel_l2(got, want)
+    print(f"    max_abs={err:.3e} rel_l2={rl:.3e}", flush=True)
+    assert err <= max_abs, f"max-abs {err:.3e} > {max_abs}"
+    assert rl <= rel_l2, f"rel-L2 {rl:.3e} > {rel_l2}"
+    return err, rl
+
+
+def index_mismatches(got_idx: np.ndarray, want_idx: np.ndarray) -> int:
+    return int((got_idx != want_idx).any(axis=1).sum())

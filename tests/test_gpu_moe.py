@@ -1,0 +1,393 @@
+"""MoE-FFN parity on the GPU, through the C ABI, against the oracle on the
+same seeded inputs.
+
+Bars: top-k expert indices identical to the oracle's (its sequential-sum
+logits) barring exact ties; combined outputs within max-abs 2e-3 and rel-L2
+1e-3 of the FP32 oracle; bucketing identical."""
+import numpy as np
+import pytest
+
+import _oracle as O
+from _cases import Case, assert_close, index_mismatches
+from qw3_amd import ds3
+from qw3_amd import workload as W
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def real():
+    """Config-1/4 layer: Q4_K gate/up, Q6_K down, FP32 router N(0, 0.02)."""
+    print("  building Q4_K/Q6_K layer", flush=True)
+    return Case(W.config_spec(1))
+
+
+@pytest.fixture(scope="module")
+def uniform():
+    """Config-2 layer: router U(-a, a)."""
+    print("  building config-2 layer", flush=True)
+    return Case(W.config_spec(2), seed=2024)
+
+
+@pytest.fixture(scope="module")
+def zipf():
+    print("  building config-3 layer (Zipf bias)", flush=True)
+    return Case(W.config_spec(3), seed=2025)
+
+
+@pytest.fixture(scope="module")
+def q80():
+    print("  building config-5 layer (all Q8_0)", flush=True)
+    return Case(W.config_spec(5), seed=2026)
+
+
+def oracle_route(case: Case, x: np.ndarray, k: int = W.N_USED):
+    idx = np.empty((x.shape[0], k), np.int32)
+    sc = np.empty((x.shape[0], k), np.float32)
+    for t in range(x.shape[0]):
+        lg = O.vec_matmul(x[t], case.wr)
+        idx[t], sc[t] = O.route(lg, k)
+    return idx, sc
+
+
+def gpu_route(case: Case, x: np.ndarray, k: int = W.N_USED):
+    T = x.shape[0]
+    s = case.spec
+    xb = ds3.Buffer.from_array(x)
+    ib, sb = ds3.Buffer.alloc(T * k * 4), ds3.Buffer.alloc(T * k * 4)
+    ds3.moe_route(xb, case.dev.router, s.router_type, T, s.n_embd, s.n_expert, k, ib, sb)
+    return ib.read(np.int32, (T, k)), sb.read(np.float32, (T, k))
+
+
+# ---------------------------------------------------------------------------
+# routing
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("cfg,T", [("real", 64), ("uniform", 512), ("zipf", 2048), ("q80", 256)])
+def test_route_indices_bit_exact(hip_ready, request, cfg, T):
+    case = request.getfixturevalue(cfg)
+    x = W.make_inputs({"real": 1, "uniform": 2, "zipf": 3, "q80": 5}[cfg], T, seed=77)
+    print(f"  route {cfg} T={T}", flush=True)
+    gi, gs = gpu_route(case, x)
+    oi, osc = oracle_route(case, x)
+    assert index_mismatches(gi, oi) == 0
+    assert np.allclose(gs, osc, rtol=2e-6, atol=1e-7)
+
+
+def test_route_guard_resolves_near_ties(hip_ready):
+    """Two router rows that differ in one far-down bit give logits within
+    rounding noise of each other; the margin guard must recompute them in
+    the reference's order and pick what the reference picks."""
+    rng = np.random.default_rng(5)
+    wr = (rng.standard_normal((16, 2048)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((64, 2048)).astype(np.float32)
+    # rows 3 and 5 become near-copies of row 0: near-ties at the top for every token
+    for r in (3, 5):
+        wr[r] = wr[0]
+        wr[r, rng.integers(0, 2048, 4)] *= np.float32(1 + 2 ** -20)
+    router = ds3.Buffer.from_array(wr)
+    before = ds3.guard_count()
+    xb = ds3.Buffer.from_array(x)
+    ib, sb = ds3.Buffer.alloc(64 * 4 * 4), ds3.Buffer.alloc(64 * 4 * 4)
+    ds3.moe_route(xb, router, ds3.TYPE_F32, 64, 2048, 16, 4, ib, sb)
+    gi = ib.read(np.int32, (64, 4))
+    oi = np.stack([O.route(O.vec_matmul(x[t], wr), 4)[0] for t in range(64)])
+    assert ds3.guard_count() > before
+    assert index_mismatches(gi, oi) == 0
+
+
+def test_topk_batch_entry_points(hip_ready):
+    rng = np.random.default_rng(11)
+    L, T, E, k = 3, 5, 128, 8
+    lg = rng.standard_normal((L, T, E)).astype(np.float32)
+    lb = ds3.Buffer.from_array(lg)
+    ib, sb = ds3.Buffer.alloc(L * T * k * 4), ds3.Buffer.alloc(L * T * k * 4)
+    from qw3_amd._native import hip
+    assert hip().ds3_hip_moe_router_topk_batch_tokens(lb.handle, ib.handle, sb.handle, L, T, E, k, True) == 0
+    gi, gs = ib.read(np.int32, (L, T, k)), sb.read(np.float32, (L, T, k))
+    assert hip().ds3_hip_moe_router_topk_batch(lb.handle, ib.handle, sb.handle, L * T, E, k, False) == 0
+    gi2, gs2 = ib.read(np.int32, (L * T, k)), sb.read(np.float32, (L * T, k))
+    for r in range(L * T):
+        oi, osc = O.route(lg.reshape(-1, E)[r], k, norm=True)
+        assert np.array_equal(gi.reshape(-1, k)[r], oi)
+        assert np.allclose(gs.reshape(-1, k)[r], osc, rtol=2e-6)
+        oi2, osc2 = O.route(lg.reshape(-1, E)[r], k, norm=False)
+        assert np.array_equal(gi2[r], oi2) and np.allclose(gs2[r], osc2, rtol=2e-6)
+
+
+# ---------------------------------------------------------------------------
+# bucketing
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("T", [1, 37, 512, 2048])
+def test_bucket_matches_oracle(hip_ready, T):
+    rng = np.random.default_rng(T)
+    E, k = 128, 8
+    p = rng.random(E) ** 4                      # skewed popularity
+    idx = np.stack([rng.choice(E, k, replace=False, p=p / p.sum()) for _ in range(T)]).astype(np.int32)
+    sc = rng.random((T, k)).astype(np.float32)
+    print(f"  bucket T={T}", flush=True)
+    bufs = [ds3.Buffer.alloc(n * 4) for n in (E, E + 1, T * k, T * k, T * k)]
+    ds3.moe_bucket(ds3.Buffer.from_array(idx), ds3.Buffer.from_array(sc), T, k, E, *bufs)
+    counts, offsets, ids, wts, pos = (b.read(dt, n) for b, dt, n in zip(
+        bufs, (np.int32, np.int32, np.int32, np.float32, np.int32), (E, E + 1, T * k, T * k, T * k)))
+    oc, oo, oids, owts, opos = O.bucket(idx, sc, E)
+    assert np.array_equal(counts, oc) and np.array_equal(offsets[:E], oo) and offsets[E] == T * k
+    assert np.array_equal(ids, oids) and np.array_equal(wts, owts) and np.array_equal(pos, opos)
+
+
+# ---------------------------------------------------------------------------
+# full FFN, device-routed
+# ---------------------------------------------------------------------------
+
+def test_decode_T1_config1(hip_ready, real):
+    """Config 1: single-token decode, 8 independent tokens, one call each."""
+    x = W.make_inputs(1, 8, seed=101)
+    want, oi, osc, _ = real.oracle(x)
+    got = np.empty_like(want)
+    for t in range(8):
+        print(f"  decode T=1 token {t}", flush=True)
+        o, gi, gs, _ = real.gpu_batch(x[t:t + 1])
+        assert np.array_equal(gi[0], oi[t])
+        got[t] = o[0]
+    err, rl = assert_close(got, want)
+    assert rl < 1e-5           # the fp32 GEMV path is far inside the bar
+
+
+def test_prefill_T512_config2(hip_ready, uniform):
+    x = W.make_inputs(2, 512, seed=102)
+    print("  prefill T=512", flush=True)
+    got, gi, gs, _ = uniform.gpu_batch(x)
+    want, oi, osc, _ = uniform.oracle(x)
+    assert index_mismatches(gi, oi) == 0
+    assert_close(got, want)
+
+
+def test_prefill_T2048_skewed_config3(hip_ready, zipf):
+    x = W.make_inputs(3, 2048, seed=103)
+    print("  prefill T=2048 skewed", flush=True)
+    got, gi, gs, _ = zipf.gpu_batch(x)
+    want, oi, osc, _ = zipf.oracle(x)
+    assert index_mismatches(gi, oi) == 0
+    counts = np.bincount(oi.reshape(-1), minlength=128)
+    print(f"    skew: top expert {counts.max()} slots ({counts.max() / oi.size:.1%}), "
+          f"{(counts == 0).sum()} experts empty, {((counts >= 1) & (counts <= 2)).sum()} with 1-2", flush=True)
+    assert (counts == 0).sum() > 0            # the empty-expert path runs
+    assert_close(got, want)
+
+
+@pytest.mark.parametrize("T", [1, 4, 16, 64, 256, 1024])
+def test_q8_0_sweep_config5(hip_ready, q80, T):
+    x = W.make_inputs(5, T, seed=104 + T)
+    print(f"  Q8_0 T={T}", flush=True)
+    got, gi, gs, _ = q80.gpu_batch(x)
+    want, oi, osc, _ = q80.oracle(x)
+    assert index_mismatches(gi, oi) == 0
+    assert_close(got, want)
+
+
+def test_decode_and_prefill_paths_agree(hip_ready, real):
+    x = W.make_inputs(2, 64, seed=105)
+    want, oi, _, _ = real.oracle(x)
+    a, ai, _, _ = real.gpu_batch(x, prefill_min=1 << 30)     # GEMV path
+    b, bi, _, _ = real.gpu_batch(x, prefill_min=1)           # grouped MFMA path
+    assert np.array_equal(ai, oi) and np.array_equal(bi, oi)
+    assert_close(a, want, rel_l2=1e-5)
+    assert_close(b, want)
+
+
+def test_residual_and_accumulate(hip_ready, real):
+    """output accumulates into what the caller left there, then + residual
+    (reference ds3_metal.h:323 and the engine's residual add, src/ds3_engine.c:1019)."""
+    x = W.make_inputs(2, 32, seed=106)
+    res = W.fill(W.NORMAL, 3, 99, 32 * 2048, 0.0, 1.0).reshape(32, 2048)
+    want, _, _, _ = real.oracle(x)
+    for pm in (1, 1 << 30):
+        got, _, _, _ = real.gpu_batch(x, residual=res, prefill_min=pm)
+        assert_close(got - res, want, max_abs=3e-3, rel_l2=1.2e-3)
+
+
+# ---------------------------------------------------------------------------
+# ds3_metal.h entry points (reference tests/test_moe_metal.c cases)
+# ---------------------------------------------------------------------------
+
+def _metal_case(name, n_embd, n_expert, n_used, n_ff, gt, ut, dt, tol, seed):
+    spec = W.LayerSpec(gt, ut, dt, ds3.TYPE_F32, W.UNIFORM, 0.5 / np.sqrt(3), n_embd, n_ff, n_expert)
+    case = Case(spec, seed=seed)
+    x = W.fill(W.UNIFORM, seed, 1, n_embd, -0.5, 0.5).reshape(1, n_embd)
+    want, oi, _, _ = case.oracle(x, n_used=n_used)
+    out = ds3.Buffer.alloc(n_embd * 4)
+    out.zero()
+    logits = ds3.Buffer.alloc(n_expert * 4)
+    print(f"  moe_ffn {name}", flush=True)
+    ds3.moe_ffn(ds3.Buffer.from_array(x), case.dev.router, ds3.TYPE_F32, case.dev.experts, out, logits,
+                n_expert, n_used)
+    got = out.read(np.float32, (1, n_embd))
+    assert float(np.abs(got - want).max()) < tol
+    return case, x, want
+
+
+@pytest.mark.parametrize("name,shape,types,tol", [
+    ("small_f32", (256, 16, 4, 128), (0, 0, 0), 1e-3),            # test_moe_metal.c:26-118
+    ("qwen3_dims_f32", (2048, 128, 8, 768), (0, 0, 0), 1e-3),    # :120-212
+    ("qwen3_dims_q4k", (2048, 128, 8, 768), (12, 12, 12), 2e-3),  # :214-365
+    ("qwen3_dims_mixed", (2048, 128, 8, 768), (12, 12, 0), 2e-3),  # :369-505
+    ("qwen3_dims_q4k_q6k", (2048, 128, 8, 768), (12, 12, 14), 2e-3),  # :509-659
+    ("q4k_gate_q8_up", (2048, 32, 4, 768), (12, 8, 14), 2e-3),    # mixed gate/up types: unfused fallback
+])
+def test_moe_ffn_entry_point(hip_ready, name, shape, types, tol):
+    _metal_case(name, *shape, *types, tol, seed=70 + len(name))
+
+
+def test_moe_ffn_experts_host_indices(hip_ready, real):
+    x = W.make_inputs(1, 1, seed=107)
+    want, oi, osc, _ = real.oracle(x)
+    out = ds3.Buffer.alloc(2048 * 4)
+    out.zero()
+    scratch = ds3.Buffer.alloc(768 * 4)
+    gs, us, dsd = real.dev.experts.strides
+    from qw3_amd._native import hip
+    import ctypes as C
+    ii = np.ascontiguousarray(oi[0], np.int32)
+    ss = np.ascontiguousarray(osc[0], np.float32)
+    rc = hip().ds3_hip_moe_ffn_experts(
+        ds3.Buffer.from_array(x).handle, real.dev.experts.gate.handle, real.dev.experts.up.handle,
+        real.dev.experts.down.handle, 12, 12, 14, gs, us, dsd, None, None, None, 0, 0, 0, 0, 0, 0,
+        out.handle, scratch.handle, scratch.handle, scratch.handle, 2048, 8, 768, 0,
+        ii.ctypes.data_as(C.POINTER(C.c_int32)), ss.ctypes.data_as(C.POINTER(C.c_float)))
+    assert rc == 0
+    assert_close(out.read(np.float32, (1, 2048)), want, rel_l2=1e-5)
+
+
+def test_expert_offset_table(hip_ready, real):
+    """expert_offsets [E][3] (reference ds3_metal.h:325-329) addresses the same bytes."""
+    gs, us, dsd = real.dev.experts.strides
+    tbl = np.array([[e * 768 * gs, e * 768 * us, e * 2048 * dsd] for e in range(128)], np.uint64)
+    x = W.make_inputs(2, 48, seed=108)
+    want, _, _, _ = real.oracle(x)
+    for pm in (1, 1 << 30):
+        T = 48
+        out = ds3.Buffer.alloc(T * 2048 * 4)
+        ds3.moe_ffn_batch(ds3.Buffer.from_array(x), real.dev.router, 0, real.dev.experts, out, T, 128, 8,
+                          expert_offsets=ds3.Buffer.from_array(tbl))
+        assert_close(out.read(np.float32, (T, 2048)), want)
+
+
+def test_shared_expert(hip_ready):
+    K, E, k, Fd, Fs = 512, 16, 4, 256, 768
+    spec = W.LayerSpec(12, 12, 14, 0, W.NORMAL, 0.05, K, Fd, E)
+    case = Case(spec, seed=9)
+    sh = Case(W.LayerSpec(12, 12, 14, 0, W.NORMAL, 0.05, K, Fs, 1), seed=10)
+    x = W.fill(W.NORMAL, 1, 1, K, 0.0, 1.0).reshape(1, K)
+    out_ref = np.empty(K, np.float32)
+    lg, sc, idx = np.empty(E, np.float32), np.empty(k, np.float32), np.empty(k, np.int32)
+    O.orc().orc_moe_ffn(O.ptr(x), O.ptr(case.wr), O.ptr(case.wg), O.ptr(case.wu), O.ptr(case.wd),
+                        O.ptr(sh.wg), O.ptr(sh.wu), O.ptr(sh.wd), O.ptr(out_ref), O.ptr(lg), O.ptr(sc), O.ptr(idx),
+                        K, E, k, Fd, Fs, True)
+    out = ds3.Buffer.alloc(K * 4)
+    out.zero()
+    ds3.moe_ffn(ds3.Buffer.from_array(x), case.dev.router, 0, case.dev.experts, out, ds3.Buffer.alloc(E * 4), E, k,
+                shared=sh.dev.experts, n_ff_shared=Fs)
+    assert_close(out.read(np.float32, (1, K)), out_ref.reshape(1, K), rel_l2=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# products and elementwise entry points
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("t,M,N,K,tol", [(8, 32, 128, 256, 2e-4), (12, 16, 64, 256, 2e-4), (14, 16, 64, 256, 3e-4),
+                                         (12, 1, 4096, 2048, 2e-4), (14, 33, 2048, 768, 3e-4)])
+def test_matmul_quantized_batch(hip_ready, t, M, N, K, tol):
+    """Reference tests/test_matmul_quant_metal.c:633-907 tolerances."""
+    rng = np.random.default_rng(M * N + K)
+    A = (rng.random((M, K)) - 0.5).astype(np.float32)
+    raw = W.quant_matrix(t, W.UNIFORM, 3, t, N, K, -0.5, 0.5)
+    Wf = O.dequantize(t, raw, N * K).reshape(N, K)
+    want = np.stack([O.vec_matmul(A[m], Wf) for m in range(M)])
+    wb = ds3.Buffer.alloc(raw.nbytes + 512)
+    wb.write(raw, offset=512)
+    cb = ds3.Buffer.alloc(M * N * 4)
+    from qw3_amd._native import hip
+    assert hip().ds3_hip_matmul_quantized_batch(ds3.Buffer.from_array(A).handle, wb.handle, cb.handle, M, N, K,
+                                                ds3.row_bytes(t, K), 512, t) == 0
+    assert float(np.abs(cb.read(np.float32, (M, N)) - want).max()) < tol
+
+
+@pytest.mark.parametrize("t", [8, 12, 14])
+def test_vec_matmul_quantized(hip_ready, t):
+    rng = np.random.default_rng(t)
+    x = (rng.random(2048) - 0.5).astype(np.float32)
+    raw = W.quant_matrix(t, W.UNIFORM, 4, t, 1024, 2048, -0.5, 0.5)
+    want = O.vec_matmul(x, O.dequantize(t, raw, 1024 * 2048).reshape(1024, 2048))
+    yb = ds3.Buffer.alloc(1024 * 4)
+    from qw3_amd._native import hip
+    fn = {8: "q8_0", 12: "q4k", 14: "q6k"}[t]
+    assert hip().ds3_hip_vec_matmul_quantized(ds3.Buffer.from_array(x).handle, ds3.Buffer.from_array(raw).handle,
+                                              yb.handle, 2048, 1024, ds3.row_bytes(t, 2048), t) == 0
+    assert float(np.abs(yb.read(np.float32, 1024) - want).max()) < 1e-4
+    assert getattr(hip(), f"ds3_hip_vec_matmul_{fn}_simd")(ds3.Buffer.from_array(x).handle,
+                                                           ds3.Buffer.from_array(raw).handle, yb.handle, 2048, 1024,
+                                                           ds3.row_bytes(t, 2048)) == 0
+    assert float(np.abs(yb.read(np.float32, 1024) - want).max()) < 1e-4
+
+
+def test_elementwise_entry_points(hip_ready):
+    from qw3_amd._native import hip
+    rng = np.random.default_rng(2)
+    n, cols, count = 4096, 64, 20
+    a, b = rng.standard_normal(n).astype(np.float32), rng.standard_normal(n).astype(np.float32)
+    ab, bb, cb = ds3.Buffer.from_array(a), ds3.Buffer.from_array(b), ds3.Buffer.alloc(n * 4)
+    assert hip().ds3_hip_vec_add(ab.handle, bb.handle, cb.handle, n) == 0
+    assert np.array_equal(cb.read(np.float32, n), a + b)
+    assert hip().ds3_hip_vec_add_inplace(ab.handle, bb.handle, n) == 0
+    assert np.array_equal(ab.read(np.float32, n), a + b)
+    assert hip().ds3_hip_buffer_copy_f32(bb.handle, cb.handle, n * 4) == 0
+    assert np.array_equal(cb.read(np.float32, n), b)
+    assert hip().ds3_hip_buffer_zero_f32(cb.handle, n * 4) == 0
+    assert not cb.read(np.float32, n).any()
+    assert hip().ds3_hip_silu_mul_f32(bb.handle, ds3.Buffer.from_array(a).handle, cb.handle, n) == 0
+    want = np.empty(n, np.float32)
+    O.orc().orc_silu(O.ptr(b), O.ptr(want), n)
+    assert np.allclose(cb.read(np.float32, n), want * a, rtol=2e-6, atol=1e-7)
+    src = rng.standard_normal((50, cols)).astype(np.float32)
+    ids = np.array([7] + list(rng.choice(50, count, replace=False)), np.int32)
+    sc = np.concatenate([[9.0], rng.random(count)]).astype(np.float32)
+    dst = ds3.Buffer.alloc(count * cols * 4)
+    assert hip().ds3_hip_gather_rows_f32(ds3.Buffer.from_array(src).handle, ds3.Buffer.from_array(ids).handle,
+                                         dst.handle, cols, count, 1) == 0
+    g = dst.read(np.float32, (count, cols))
+    assert np.array_equal(g, src[ids[1:]])
+    base = rng.standard_normal((50, cols)).astype(np.float32)
+    db = ds3.Buffer.from_array(base)
+    assert hip().ds3_hip_scatter_add_weighted_f32(dst.handle, ds3.Buffer.from_array(sc).handle,
+                                                  ds3.Buffer.from_array(ids).handle, db.handle, cols, count, 1) == 0
+    want = base.copy()
+    want[ids[1:]] += sc[1:, None] * g
+    assert np.allclose(db.read(np.float32, (50, cols)), want, rtol=1e-6, atol=1e-6)
+
+
+def test_invalid_arguments_return_error(hip_ready, real):
+    """Argument rules of reference src/ds3_metal.m:1841-1862, 2453-2485:
+    -1 and output untouched."""
+    from qw3_amd._native import hip
+    x = ds3.Buffer.from_array(np.ones(2048, np.float32))
+    out = ds3.Buffer.from_array(np.full(2048, 7.0, np.float32))
+    lg = ds3.Buffer.alloc(128 * 4)
+    s = ds3.Buffer.alloc(4096)
+    e = real.dev.experts
+    gs, us, dsd = e.strides
+
+    def call(gt=12, ut=12, dt=14, n_embd=2048, n_used=8, n_expert=128, n_ff=768, eu=s, ed=s, rt=0):
+        return hip().ds3_hip_moe_ffn(x.handle, real.dev.router.handle, e.gate.handle, e.up.handle, e.down.handle,
+                                     gt, ut, dt, gs, us, dsd, None, None, None, 0, 0, 0, 0, 0, 0,
+                                     out.handle, lg.handle, None, s.handle, eu and eu.handle, ed and ed.handle,
+                                     n_embd, n_expert, n_used, n_ff, 0, 2048 * 4, rt, True)
+    assert call(gt=99) == -1                    # unsupported type
+    assert call(dt=14, n_ff=700) == -1           # K-quant in_dim % 256
+    assert call(n_used=129) == -1               # n_used > n_expert
+    assert call(n_used=0) == -1
+    assert call(eu=None) == -1                  # quantised path needs expert_up/expert_down
+    assert np.all(out.read(np.float32, 2048) == 7.0)
+    assert hip().ds3_hip_matmul_quantized_batch(x.handle, e.gate.handle, out.handle, 1, 4, 100, 144, 0, 12) == -1
+    assert hip().ds3_hip_buffer_zero_f32(out.handle, 6) == -1
+    assert hip().ds3_hip_dequantize(x.handle, 0, 12, 100, out.handle) == -1
