@@ -42,7 +42,11 @@ def _check(rc: int, what: str) -> None:
 
 
 class Buffer:
-    """A ds3_hip_buffer_t handle.  Frees its memory when closed or collected."""
+    """A ds3_hip_buffer_t handle.  Frees its memory when closed or collected.
+
+    Pass the Buffer object itself to ctypes calls (it converts through
+    _as_parameter_ and stays referenced for the duration of the call); never
+    keep the raw handle of a Buffer that may be collected."""
 
     def __init__(self, handle: int, nbytes: int, owner: bool = True):
         if not handle:
@@ -50,6 +54,10 @@ class Buffer:
         self.handle = C.c_void_p(handle)
         self.nbytes = nbytes
         self._owner = owner
+
+    @property
+    def _as_parameter_(self):
+        return self.handle
 
     @classmethod
     def alloc(cls, nbytes: int) -> "Buffer":
@@ -90,7 +98,7 @@ class Buffer:
 
 
 def _h(b):
-    return b.handle if b is not None else None
+    return b if b is not None else None
 
 
 @dataclass
@@ -113,21 +121,21 @@ class ExpertTensors:
 
 
 def dequantize(src: Buffer, type_: int, n: int, dst: Buffer, src_offset: int = 0) -> None:
-    _check(hip().ds3_hip_dequantize(src.handle, src_offset, type_, n, dst.handle), "dequantize")
+    _check(hip().ds3_hip_dequantize(src, src_offset, type_, n, dst), "dequantize")
 
 
 def moe_route(x: Buffer, router: Buffer, router_type: int, n_tokens: int, n_embd: int, n_expert: int,
               n_used: int, indices: Buffer, scores: Buffer, logits: Buffer | None = None,
               norm: bool = True) -> None:
-    _check(hip().ds3_hip_moe_route(x.handle, router.handle, _h(logits), indices.handle, scores.handle,
+    _check(hip().ds3_hip_moe_route(x, router, _h(logits), indices, scores,
                                    n_tokens, n_embd, n_expert, n_used, row_bytes(router_type, n_embd),
                                    router_type, norm), "moe_route")
 
 
 def moe_bucket(indices: Buffer, scores: Buffer, n_tokens: int, n_used: int, n_expert: int,
                counts: Buffer, offsets: Buffer, ids: Buffer, wts: Buffer, slot_pos: Buffer) -> None:
-    _check(hip().ds3_hip_moe_bucket(indices.handle, scores.handle, n_tokens, n_used, n_expert, counts.handle,
-                                    offsets.handle, ids.handle, wts.handle, slot_pos.handle), "moe_bucket")
+    _check(hip().ds3_hip_moe_bucket(indices, scores, n_tokens, n_used, n_expert, counts,
+                                    offsets, ids, wts, slot_pos), "moe_bucket")
 
 
 def moe_ffn_batch(x: Buffer, router: Buffer, router_type: int, ex: ExpertTensors, out: Buffer, n_tokens: int,
@@ -136,9 +144,9 @@ def moe_ffn_batch(x: Buffer, router: Buffer, router_type: int, ex: ExpertTensors
                   expert_offsets: Buffer | None = None) -> None:
     gs, us, ds = ex.strides
     _check(hip().ds3_hip_moe_ffn_batch(
-        x.handle, router.handle, ex.gate.handle, ex.up.handle, ex.down.handle,
+        x, router, ex.gate, ex.up, ex.down,
         ex.gate_type, ex.up_type, ex.down_type, gs, us, ds, _h(expert_offsets),
-        out.handle, _h(residual), _h(logits), _h(indices), _h(scores),
+        out, _h(residual), _h(logits), _h(indices), _h(scores),
         n_tokens, ex.n_embd, n_expert, n_used, ex.n_ff, row_bytes(router_type, ex.n_embd), router_type, norm),
         "moe_ffn_batch")
 
@@ -150,7 +158,7 @@ def moe_ffn(x: Buffer, router: Buffer, router_type: int, ex: ExpertTensors, out:
     gs, us, ds = ex.strides
     scratch = scratch or Buffer.alloc(4 * max(ex.n_ff, ex.n_embd, n_ff_shared, 1))
     if shared is not None:
-        sg, su, sd = shared.gate.handle, shared.up.handle, shared.down.handle
+        sg, su, sd = shared.gate, shared.up, shared.down
         sgt, sut, sdt = shared.gate_type, shared.up_type, shared.down_type
         sgs, sus = row_bytes(sgt, ex.n_embd), row_bytes(sut, ex.n_embd)
         sds = row_bytes(sdt, n_ff_shared)
@@ -159,10 +167,10 @@ def moe_ffn(x: Buffer, router: Buffer, router_type: int, ex: ExpertTensors, out:
         sgt = sut = sdt = TYPE_F32
         sgs = sus = sds = 0
     _check(hip().ds3_hip_moe_ffn(
-        x.handle, router.handle, ex.gate.handle, ex.up.handle, ex.down.handle,
+        x, router, ex.gate, ex.up, ex.down,
         ex.gate_type, ex.up_type, ex.down_type, gs, us, ds,
         sg, su, sd, sgt, sut, sdt, sgs, sus, sds,
-        out.handle, logits.handle, _h(expert_offsets), scratch.handle, scratch.handle, scratch.handle,
+        out, logits, _h(expert_offsets), scratch, scratch, scratch,
         ex.n_embd, n_expert, n_used, ex.n_ff, n_ff_shared, row_bytes(router_type, ex.n_embd), router_type, norm),
         "moe_ffn")
 

@@ -120,13 +120,13 @@ def vec_matmul(x: np.ndarray, W: np.ndarray) -> np.ndarray:
     return y
 
 
-def route(logits: np.ndarray, k: int, norm: bool = True):
+def route(logits: np.ndarray, k: int, norm: bool = True, with_probs: bool = False):
     """softmax -> top-k -> renorm of one token's logits (copy)."""
     lg = np.array(logits, np.float32)
     idx = np.empty(k, np.int32)
     sc = np.empty(k, np.float32)
     orc().orc_route(ptr(lg), lg.size, k, norm, ptr(idx), ptr(sc))
-    return idx, sc
+    return (idx, sc, lg) if with_probs else (idx, sc)
 
 
 def moe_tokens(x: np.ndarray, wr: np.ndarray, wg: np.ndarray, wu: np.ndarray, wd: np.ndarray,
