@@ -1,0 +1,246 @@
+"""MoE-FFN throughput on one MI355X (benchmark contract: one JSON line on stdout).
+
+Workload: one Qwen3-30B-A3B MoE-FFN layer call on
+T = 512 tokens -- router, softmax/top-8, bucketing, grouped Q4_K gate/up and
+Q6_K down products, SwiGLU and the weighted combine -- through the C ABI
+(ds3_hip_moe_ffn_batch).  A step is one layer call on one batch; the engine's
+output zeroing (reference src/ds3_engine.c:902) is part of the step.  Layers
+are cycled from `--layers` distinct resident copies so weights cannot stay in
+the 256 MB Infinity Cache between steps.  The line also carries the T = 1
+decode figures (configs[0] shape) under "t1".
+
+roofline: the dominant kernel's algorithmic bytes per launch / its mean
+duration, timed with HIP events on the library stream inside the timed region.
+cpu_baseline: the reference's own ds3_ref_moe_ffn (compiled from its sources
+into oracle/_ref) on the host cores, FP32-dequantised weights resident, on a
+bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
+FP16_PEAK_TFLOPS = 2500.0      # dense fp16 MFMA
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--tokens", type=int, default=512)
+    p.add_argument("--layers", type=int, default=8, help="distinct resident layers cycled per step")
+    p.add_argument("--config", type=int, default=2, choices=(2, 3, 5))
+    p.add_argument("--t1-steps", type=int, default=200)
+    p.add_argument("--no-t1", action="store_true")
+    p.add_argument("--no-cpu", action="store_true")
+    p.add_argument("--cpu-tokens", type=int, default=512)
+    p.add_argument("--traffic", type=str, default=None,
+                   help="JSON {kernel: bytes_per_launch} measured by rocprofv3 --pmc (profiles/)")
+    return p.parse_args()
+
+
+def kernel_bytes(name, spec, T, counts, n_used):
+    """Algorithmic HBM bytes of one launch of `name` (per-kernel split of the
+    layer's algorithmic bytes; see DESIGN.md, Measurement)."""
+    from qw3_amd import ds3
+    from qw3_amd import workload as W
+    E, K, F = spec.n_expert, spec.n_embd, spec.n_ff
+    distinct = int((counts > 0).sum())
+    gu = F * (ds3.row_bytes(spec.gate_type, K) + ds3.row_bytes(spec.up_type, K))
+    dn = K * ds3.row_bytes(spec.down_type, F)
+    S = T * n_used
+    return {
+        "moe_grouped_gate_up": distinct * gu + T * K * 2 + S * F * 2,
+        "moe_grouped_down": distinct * dn + S * F * 2 + S * K * 4,
+        "moe_decode_gate_up": distinct * gu + T * K * 4 + S * F * 4,
+        "moe_decode_down": distinct * dn + S * F * 4 + T * K * 4,
+        "router_logits": W.router_bytes(spec) + T * K * 4 + T * E * 4,
+    }.get(name)
+
+
+def run_gpu(args, T, steps, warmup, layers, xs, spec, n_used=8):
+    from qw3_amd import ds3
+    from qw3_amd._native import hip
+    E, K = spec.n_expert, spec.n_embd
+    out = ds3.Buffer.alloc(T * K * 4)
+    idx = ds3.Buffer.alloc(T * n_used * 4)
+
+    def step(i):
+        d = layers[i % len(layers)]
+        out.zero()
+        ds3.moe_ffn_batch(xs[i % len(xs)], d.router, spec.router_type, d.experts, out, T, E, n_used,
+                          indices=idx if i == 0 else None)
+
+    hip().ds3_hip_begin_batch()
+    for i in range(warmup):
+        step(i)
+    hip().ds3_hip_end_batch()
+    counts = np.bincount(idx.read(np.int32, (T, n_used)).reshape(-1), minlength=E)
+    # timed region: synchronise, K steps enqueued back to back, synchronise
+    hip().ds3_hip_kernel_timing_reset()
+    hip().ds3_hip_kernel_timing(1)
+    hip().ds3_hip_synchronize()
+    hip().ds3_hip_begin_batch()
+    t0 = time.perf_counter()
+    hip().ds3_hip_timer_start()
+    for i in range(steps):
+        step(i)
+    gpu_ms = hip().ds3_hip_timer_stop_ms()
+    hip().ds3_hip_end_batch()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    hip().ds3_hip_kernel_timing(0)
+    stats = ds3.kernel_stats()
+    return wall_ms, gpu_ms, stats, counts
+
+
+def roofline(stats, spec, T, counts, n_used, traffic):
+    name = max((k for k in stats if kernel_bytes(k, spec, T, counts, n_used) is not None),
+               key=lambda k: stats[k][1])
+    n, ms = stats[name]
+    avg_s = ms / n / 1e3
+    b = kernel_bytes(name, spec, T, counts, n_used)
+    achieved = b / avg_s / 1e9
+    r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
+         "kernel_avg_us": round(avg_s * 1e6, 2), "alg_bytes_per_launch": b}
+    if traffic and name in traffic:
+        r["traffic"] = traffic[name]
+    return r
+
+
+def cpu_baseline(layer, x, n_used, n_tokens):
+    """ds3_ref_moe_ffn (reference build, else the oracle port) per token on
+    host threads; ctypes releases the GIL during each call."""
+    import concurrent.futures as cf
+    import ctypes as C
+    sys.path.insert(0, str(ROOT / "tests"))
+    import _oracle as O
+    spec = layer.spec
+    E, K, F = spec.n_expert, spec.n_embd, spec.n_ff
+    kind = "reference" if O.ref() is not None else "port"
+    deq = O.ref_dequantize if kind == "reference" else O.dequantize
+    t0 = time.perf_counter()
+    wr = deq(spec.router_type, layer.router, E * K) if spec.router_type != 0 else layer.router.view(np.float32)
+    wg = deq(spec.gate_type, layer.gate, E * F * K)
+    wu = deq(spec.up_type, layer.up, E * F * K)
+    wd = deq(spec.down_type, layer.down, E * K * F)
+    log(f"[bench] cpu baseline: dequantised layer in {time.perf_counter() - t0:.1f}s ({kind})")
+    fn = O.ref().ds3_ref_moe_ffn if kind == "reference" else O.orc().orc_moe_ffn
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    xt = np.ascontiguousarray(x[:n_tokens])
+    out = np.empty_like(xt)
+
+    def work(r):
+        lg = np.empty(E, np.float32)
+        sc = np.empty(n_used, np.float32)
+        ix = np.empty(n_used, np.int32)
+        for t in r:
+            fn(O.ptr(xt[t]), O.ptr(wr), O.ptr(wg), O.ptr(wu), O.ptr(wd), None, None, None, O.ptr(out[t]),
+               O.ptr(lg), O.ptr(sc), O.ptr(ix), K, E, n_used, F, 0, True)
+
+    chunks = [range(i, n_tokens, threads) for i in range(threads)]
+    t0 = time.perf_counter()
+    with cf.ThreadPoolExecutor(threads) as ex:
+        list(ex.map(work, chunks))
+    dt = time.perf_counter() - t0
+    return {"value": round(n_tokens / dt, 2), "unit": "tokens/s", "cores": threads, "kind": kind,
+            "sample": f"{n_tokens} tokens of the T={x.shape[0]} batch, one layer, FP32-dequantised weights "
+                      f"resident, ds3_ref_moe_ffn per token on {threads} threads ({dt:.1f}s wall)"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "see DESIGN.md for how the MoE FFN would shard across GPUs.", file=sys.stderr)
+        sys.exit(2)
+    from qw3_amd import ds3
+    from qw3_amd import workload as W
+    ds3.init()
+    info = ds3.device_info()
+    log(f"[bench] device {info['arch']} CUs={info['n_cu']}")
+    spec = W.config_spec(args.config)
+    T, n_used = args.tokens, W.N_USED
+    t0 = time.perf_counter()
+    hosts, layers = [], []
+    for l in range(args.layers):
+        h = W.make_layer(spec, seed=1234, layer=l)
+        layers.append(h.to_device())
+        if l == 0:
+            hosts.append(h)
+    log(f"[bench] {args.layers} layers generated and resident in {time.perf_counter() - t0:.1f}s")
+    xs_host = [W.make_inputs(args.config, T, seed=99, step=s) for s in range(4)]
+    xs = [ds3.Buffer.from_array(x) for x in xs_host]
+
+    wall_ms, gpu_ms, stats, counts = run_gpu(args, T, args.steps, args.warmup, layers, xs, spec, n_used)
+    ms_step = wall_ms / args.steps
+    log(f"[bench] T={T}: {ms_step * 1e3:.1f} us/step wall, {gpu_ms / args.steps * 1e3:.1f} us/step events")
+    for k, (n, ms) in sorted(stats.items(), key=lambda kv: -kv[1][1]):
+        log(f"[bench]   {k:24s} {n:5d} launches  avg {ms / n * 1e3:8.2f} us")
+    traffic = json.loads(Path(args.traffic).read_text()) if args.traffic else None
+    rl = roofline(stats, spec, T, counts, n_used, traffic)
+    flops = W.algorithmic_flops(spec, T, n_used)
+    line = {
+        "metric": "MoE-FFN tokens/s at T=512 (T=1 under t1); HBM GB/s and MFMA util vs peak",
+        "value": round(T / (ms_step / 1e3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if args.config != 5 else "f16",
+        "data": "synthetic (seeded generator; expert weights N(0,0.02) quantised by this project's GGUF quantisers)",
+        "config": {"workload": f"configs[{args.config - 1}]: one Qwen3-30B-A3B MoE-FFN layer, T={T} gathered prefill, "
+                               f"{W.N_EXPERT} experts top-{n_used}, "
+                               f"{ds3.TYPE_NAMES[spec.gate_type]} gate/up + {ds3.TYPE_NAMES[spec.down_type]} down, "
+                               f"{ds3.TYPE_NAMES[spec.router_type]} router",
+                   "tokens": T, "n_embd": spec.n_embd, "n_ff": spec.n_ff, "layers_cycled": args.layers,
+                   "distinct_experts_step0": int((counts > 0).sum())},
+        "roofline": rl,
+        "mfma_util": round(flops / (ms_step / 1e3) / (FP16_PEAK_TFLOPS * 1e12), 4),
+        "alg_bytes_per_step": W.algorithmic_bytes(spec, T, int((counts > 0).sum())),
+    }
+    line["hbm_frac_step"] = round(line["alg_bytes_per_step"] / (ms_step / 1e3) / (HBM_PEAK_GBS * 1e9), 4)
+
+    if not args.no_t1:
+        spec1 = W.config_spec(1)
+        layers1 = layers if args.config in (1, 2) else [W.make_layer(spec1, seed=1234, layer=l).to_device()
+                                                        for l in range(args.layers)]
+        x1 = [ds3.Buffer.from_array(W.make_inputs(1, 1, seed=98, step=s)) for s in range(16)]
+        w1, g1, st1, c1 = run_gpu(args, 1, args.t1_steps, args.warmup, layers1, x1, spec1, n_used)
+        ms1 = w1 / args.t1_steps
+        log(f"[bench] T=1: {ms1 * 1e3:.1f} us/step wall")
+        for k, (n, ms) in sorted(st1.items(), key=lambda kv: -kv[1][1]):
+            log(f"[bench]   {k:24s} {n:5d} launches  avg {ms / n * 1e3:8.2f} us")
+        b1 = W.algorithmic_bytes(spec1, 1, n_used)
+        line["t1"] = {"value": round(1 / (ms1 / 1e3), 1), "unit": "tokens/s", "ms_per_step": round(ms1, 5),
+                      "steps": args.t1_steps, "alg_bytes_per_step": b1,
+                      "hbm_frac_step": round(b1 / (ms1 / 1e3) / (HBM_PEAK_GBS * 1e9), 4),
+                      "roofline": roofline(st1, spec1, 1, c1, n_used, traffic)}
+
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(hosts[0], xs_host[0], n_used, min(args.cpu_tokens, T))
+        log(f"[bench] cpu baseline {line['cpu_baseline']['value']} tok/s")
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

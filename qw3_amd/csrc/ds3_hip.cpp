@@ -581,6 +581,77 @@ bool moe_limits_ok(uint32_t n_expert, uint32_t n_used)
 
 }  // namespace
 
+namespace {
+
+struct RouteBufs {
+    float *logits;       // [T][E] logits actually used (output)
+    int32_t *idx;
+    float *scores;
+    float *wnorm2;       // [nparts][E] scratch
+    float *part;         // [nparts][T][E] scratch (MFMA router)
+};
+
+// Scratch of route_tokens beyond the output buffers.
+size_t route_scratch_bytes(int T, uint32_t n_embd, uint32_t n_expert)
+{
+    const int np = router_parts(T, (int)n_embd);
+    return ((size_t)np * n_expert * 4 + 255) / 256 * 256 + (size_t)np * T * n_expert * 4;
+}
+
+int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstride, int rtype, int T, uint32_t n_embd,
+                 uint32_t n_expert, uint32_t n_used, bool norm, const RouteBufs &rb)
+{
+    hipError_t e;
+    RouteArgs ra{};
+    if (router_mfma_ok(rtype, (int)n_embd, (int)n_expert, x, cptr(router), rstride)) {
+        const int np = router_parts(T, (int)n_embd);
+        {
+            KScope ks("router_logits");
+            e = launch_router_logits(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, np, rb.part,
+                                     rb.wnorm2, g.stream);
+        }
+        ra.logits = rb.part;
+        ra.nparts = np;
+        ra.part_stride = (int64_t)T * n_expert;
+        ra.logits_out = rb.logits;
+    } else {
+        KScope ks("router_logits");
+        e = launch_gemv(rtype, x, n_embd, cptr(router), rstride, rb.logits, n_expert, T, (int)n_expert, (int)n_embd,
+                        rb.wnorm2, g.stream);
+        ra.logits = rb.logits;
+        ra.logits_out = nullptr;
+    }
+    if (e != hipSuccess) return report(e, "router logits");
+    ra.idx = rb.idx;
+    ra.scores = rb.scores;
+    ra.T = T;
+    ra.E = (int)n_expert;
+    ra.k = (int)n_used;
+    ra.logit_stride = n_expert;
+    ra.out_stride = n_used;
+    ra.norm = norm;
+    ra.x = x;
+    ra.K = (int)n_embd;
+    ra.rtype = rtype;
+    ra.rw = cptr(router);
+    ra.rstride = rstride;
+    ra.wnorm2 = rb.wnorm2;
+    ra.guard_count = g.guard;
+    KScope ks("router_topk");
+    return report(launch_route(ra, g.stream), "router topk");
+}
+
+// Largest token chunk whose bucketing bitmaps fit in LDS.
+int prefill_chunk(uint32_t n_expert)
+{
+    int c = (int)(61440 / (6 * n_expert)) * 32;
+    if (c > 2048) c = 2048;
+    if (c < 32) c = 32;
+    return c;
+}
+
+}  // namespace
+
 // reference src/ds3_metal.m:2415-2661
 extern "C" int ds3_hip_moe_ffn(
     const ds3_hip_buffer_t *input, const ds3_hip_buffer_t *w_gate_inp, const ds3_hip_buffer_t *w_gate_exps,
@@ -625,44 +696,19 @@ extern "C" int ds3_hip_moe_ffn(
     const uint32_t ff_max = has_shared && n_ff_shared > n_ff_exp ? n_ff_shared : n_ff_exp;
     Bump bp;
     const size_t o_idx = bp.take((size_t)n_used * 4), o_sc = bp.take((size_t)n_used * 4);
-    const size_t o_wn = bp.take((size_t)n_expert * 4);
+    const size_t o_r = bp.take(route_scratch_bytes(1, n_embd, n_expert));
     const size_t o_h = bp.take((size_t)n_used * ff_max * 4), o_t = bp.take((size_t)n_used * ff_max * 4);
     uint8_t *ws = ws_get(bp.off);
     if (!ws) return -1;
     int32_t *idx = (int32_t *)(ws + o_idx);
-    float *sc = (float *)(ws + o_sc), *wn = (float *)(ws + o_wn), *h = (float *)(ws + o_h), *tmp = (float *)(ws + o_t);
+    float *sc = (float *)(ws + o_sc), *h = (float *)(ws + o_h), *tmp = (float *)(ws + o_t);
     const float *x = fptr(input);
-
-    hipError_t e;
-    {
-        KScope ks("router_logits");
-        e = launch_gemv(router_type, x, n_embd, cptr(w_gate_inp), router_row_stride, fptr(gate_logits), n_expert, 1,
-                        (int)n_expert, (int)n_embd, wn, g.stream);
-    }
-    if (e != hipSuccess) return report(e, "moe_ffn router");
-    RouteArgs ra{};
-    ra.logits = fptr(gate_logits);
-    ra.logits_out = nullptr;
-    ra.idx = idx;
-    ra.scores = sc;
-    ra.T = 1;
-    ra.E = (int)n_expert;
-    ra.k = (int)n_used;
-    ra.logit_stride = n_expert;
-    ra.out_stride = n_used;
-    ra.norm = norm_topk_prob;
-    ra.x = x;
-    ra.K = (int)n_embd;
-    ra.rtype = router_type;
-    ra.rw = cptr(w_gate_inp);
-    ra.rstride = router_row_stride;
-    ra.wnorm2 = wn;
-    ra.guard_count = g.guard;
-    {
-        KScope ks("router_topk");
-        e = launch_route(ra, g.stream);
-    }
-    if (e != hipSuccess) return report(e, "moe_ffn topk");
+    const int np = router_parts(1, (int)n_embd);
+    RouteBufs rb{ fptr(gate_logits), idx, sc, (float *)(ws + o_r),
+                  (float *)(ws + o_r + ((size_t)np * n_expert * 4 + 255) / 256 * 256) };
+    if (route_tokens(x, w_gate_inp, router_row_stride, router_type, 1, n_embd, n_expert, n_used, norm_topk_prob,
+                     rb) != 0)
+        return -1;
     if (has_shared &&
         run_shared(x, w_shared_gate, w_shared_up, w_shared_down, shared_gate_type, shared_up_type, shared_down_type,
                    shared_gate_row_stride, shared_up_row_stride, shared_down_row_stride, n_embd, n_ff_shared,
@@ -792,57 +838,6 @@ extern "C" int ds3_hip_moe_router_topk_batch_tokens(const ds3_hip_buffer_t *logi
 // Device-routed extensions
 // ===========================================================================
 
-namespace {
-
-struct RouteBufs {
-    float *logits;
-    int32_t *idx;
-    float *scores;
-    float *wnorm2;
-};
-
-int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstride, int rtype, int T, uint32_t n_embd,
-                 uint32_t n_expert, uint32_t n_used, bool norm, const RouteBufs &rb)
-{
-    hipError_t e;
-    {
-        KScope ks("router_logits");
-        e = launch_gemv(rtype, x, n_embd, cptr(router), rstride, rb.logits, n_expert, T, (int)n_expert, (int)n_embd,
-                        rb.wnorm2, g.stream);
-    }
-    if (e != hipSuccess) return report(e, "router logits");
-    RouteArgs ra{};
-    ra.logits = rb.logits;
-    ra.logits_out = nullptr;
-    ra.idx = rb.idx;
-    ra.scores = rb.scores;
-    ra.T = T;
-    ra.E = (int)n_expert;
-    ra.k = (int)n_used;
-    ra.logit_stride = n_expert;
-    ra.out_stride = n_used;
-    ra.norm = norm;
-    ra.x = x;
-    ra.K = (int)n_embd;
-    ra.rtype = rtype;
-    ra.rw = cptr(router);
-    ra.rstride = rstride;
-    ra.wnorm2 = rb.wnorm2;
-    ra.guard_count = g.guard;
-    KScope ks("router_topk");
-    return report(launch_route(ra, g.stream), "router topk");
-}
-
-// Largest token chunk whose bucketing bitmaps fit in LDS.
-int prefill_chunk(uint32_t n_expert)
-{
-    int c = (int)(61440 / (6 * n_expert)) * 32;
-    if (c > 2048) c = 2048;
-    if (c < 32) c = 32;
-    return c;
-}
-
-}  // namespace
 
 extern "C" int ds3_hip_moe_route(const ds3_hip_buffer_t *input, const ds3_hip_buffer_t *w_gate_inp,
                                  ds3_hip_buffer_t *gate_logits, ds3_hip_buffer_t *indices, ds3_hip_buffer_t *scores,
@@ -858,11 +853,12 @@ extern "C" int ds3_hip_moe_route(const ds3_hip_buffer_t *input, const ds3_hip_bu
         !fits(scores, T * n_used * 4, "scores") || !fits(gate_logits, T * n_expert * 4, "gate_logits"))
         return -1;
     Bump bp;
-    const size_t o_l = bp.take(T * n_expert * 4), o_w = bp.take((size_t)n_expert * 4);
+    const size_t o_l = bp.take(T * n_expert * 4), o_r = bp.take(route_scratch_bytes((int)T, n_embd, n_expert));
     uint8_t *ws = ws_get(bp.off);
     if (!ws) return -1;
+    const int np = router_parts((int)T, (int)n_embd);
     RouteBufs rb{ gate_logits ? fptr(gate_logits) : (float *)(ws + o_l), (int32_t *)dptr(indices), fptr(scores),
-                  (float *)(ws + o_w) };
+                  (float *)(ws + o_r), (float *)(ws + o_r + ((size_t)np * n_expert * 4 + 255) / 256 * 256) };
     if (route_tokens(fptr(input), w_gate_inp, router_row_stride, router_type, (int)T, n_embd, n_expert, n_used,
                      norm_topk_prob, rb) != 0)
         return -1;
@@ -931,7 +927,8 @@ extern "C" int ds3_hip_moe_ffn_batch(
 
     Bump bp;
     const size_t o_l = bp.take(T * n_expert * 4), o_i = bp.take(T * n_used * 4), o_s = bp.take(T * n_used * 4);
-    const size_t o_w = bp.take((size_t)n_expert * 4);
+    const size_t o_w = bp.take(route_scratch_bytes((int)T, n_embd, n_expert));
+    const int np = router_parts((int)T, (int)n_embd);
     size_t o_h = 0, o_t = 0, o_x16 = 0, o_cnt = 0, o_off = 0, o_ids = 0, o_wts = 0, o_pos = 0, o_tiles = 0, o_nt = 0,
            o_h16 = 0, o_y = 0;
     if (use_grouped) {
@@ -953,7 +950,8 @@ extern "C" int ds3_hip_moe_ffn_batch(
     if (!ws) return -1;
     RouteBufs rb{ gate_logits ? fptr(gate_logits) : (float *)(ws + o_l),
                   indices ? (int32_t *)dptr(indices) : (int32_t *)(ws + o_i),
-                  scores ? fptr(scores) : (float *)(ws + o_s), (float *)(ws + o_w) };
+                  scores ? fptr(scores) : (float *)(ws + o_s), (float *)(ws + o_w),
+                  (float *)(ws + o_w + ((size_t)np * n_expert * 4 + 255) / 256 * 256) };
     const float *x = fptr(input);
     if (route_tokens(x, w_gate_inp, router_row_stride, router_type, (int)T, n_embd, n_expert, n_used, norm_topk_prob,
                      rb) != 0)

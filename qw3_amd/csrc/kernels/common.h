@@ -270,6 +270,262 @@ __device__ __forceinline__ void unit_decode(const uint8_t *row, int u, float (&w
     }
 }
 
+// ---------------------------------------------------------------------------
+// fp16 MFMA fragments straight from codes.  A code c (0..1023) becomes the
+// fp16 value 1024 + c by OR-ing 0x6400 into its 16-bit lane (exponent 10,
+// c in the mantissa); the weight is then one fused multiply-add
+//   w = scale * (1024 + c) + (-(scale * (1024 + zero)) - min)
+// computed at fp32 precision and rounded once to fp16 (v_fma_mix{lo,hi}_f16).
+// The scale products are exact; only the folded constant rounds in fp32,
+// ~1e-5 of a weight, far below the fp16 rounding of the result.
+// ---------------------------------------------------------------------------
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// 0x64006400 in a VGPR: with the mask in an SGPR, (x & mask) | magic is then
+// a single v_and_or_b32 (gfx9 VOP3 takes no literal and one SGPR).
+__device__ __forceinline__ uint32_t vgpr_magic()
+{
+    uint32_t v;
+    asm("v_mov_b32 %0, 0x64006400" : "=v"(v));
+    return v;
+}
+
+// Four weights from one dword: codes of bytes 0 and 2 are x02 & mask, of
+// bytes 1 and 3 x13 & mask (mask keeps the low code bits of each 16-bit
+// lane).  Writes w[b0..b3] in byte order.
+__device__ __forceinline__ void fma4(uint32_t x02, uint32_t x13, uint32_t mask, uint32_t mg, float sc, float c,
+                                     _Float16 *w)
+{
+    const half2_t a = __builtin_bit_cast(half2_t, (x02 & mask) | mg);
+    const half2_t b = __builtin_bit_cast(half2_t, (x13 & mask) | mg);
+    w[0] = (_Float16)__builtin_fmaf(sc, (float)a[0], c);
+    w[1] = (_Float16)__builtin_fmaf(sc, (float)b[0], c);
+    w[2] = (_Float16)__builtin_fmaf(sc, (float)a[1], c);
+    w[3] = (_Float16)__builtin_fmaf(sc, (float)b[1], c);
+}
+
+// ---------------------------------------------------------------------------
+// Raw bytes of the two units (g, g+4) of one row in 256-wide K step s, held
+// in registers so the loads for step s+1 can be in flight while step s is
+// decoded.  decode(hv) yields unit g + 4*hv exactly as unit_decode does.
+// ---------------------------------------------------------------------------
+template <int TYPE> struct RawUnits;
+
+template <> struct RawUnits<T_Q4_K> {
+    uint4 hdr, q0, q1;
+    __device__ __forceinline__ void load(const uint8_t *row, int s, int g)
+    {
+        const uint8_t *blk = row + (size_t)s * 144;
+        hdr = *(const uint4 *)blk;
+        q0 = *(const uint4 *)(blk + 16 + 16 * g);
+        q1 = *(const uint4 *)(blk + 16 + 16 * (g + 4));
+    }
+    // fragments p = 0..3 of unit g + 4*hv: low nibbles of bytes 0-7, 8-15,
+    // then high nibbles of bytes 0-7, 8-15 (unit_decode's segment order)
+    __device__ __forceinline__ void decode_frags(int hv, int g, half8_t (&fr)[4]) const
+    {
+        const int c = g + 4 * hv;
+        const uint4 q = hv ? q1 : q0;
+        const float d = h2f(hdr.x & 0xffffu), dmin = h2f(hdr.x >> 16);
+        float sc0, mn0, sc1, mn1;
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1), sc0, mn0);
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1) + 1, sc1, mn1);
+        const float dl = d * sc0, dh = d * sc1;
+        const float cl = -(1024.0f * dl) - dmin * mn0, ch = -(1024.0f * dh) - dmin * mn1;
+        const uint32_t qw[4] = { q.x, q.y, q.z, q.w };
+        const uint32_t mg = vgpr_magic();
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            _Float16 w[8];
+#pragma unroll
+            for (int dd = 0; dd < 2; dd++) {
+                const uint32_t x = qw[2 * (p & 1) + dd];
+                if (p < 2) fma4(x, x >> 8, 0x000f000fu, mg, dl, cl, w + 4 * dd);
+                else fma4(x >> 4, x >> 12, 0x000f000fu, mg, dh, ch, w + 4 * dd);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) fr[p][i] = w[i];
+        }
+    }
+    __device__ __forceinline__ void decode(int hv, int g, float (&w)[32]) const
+    {
+        const int c = g + 4 * hv;
+        const uint4 q = hv ? q1 : q0;
+        const float d = h2f(hdr.x & 0xffffu), dmin = h2f(hdr.x >> 16);
+        float sc0, mn0, sc1, mn1;
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1), sc0, mn0);
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1) + 1, sc1, mn1);
+        const float dl = d * sc0, ml = dmin * mn0, dh = d * sc1, mh = dmin * mn1;
+        const uint32_t qw[4] = { q.x, q.y, q.z, q.w };
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float a0, a1, a2, a3;
+            cvt4(qw[i] & 0x0f0f0f0fu, a0, a1, a2, a3);
+            w[4 * i + 0] = dl * a0 - ml; w[4 * i + 1] = dl * a1 - ml;
+            w[4 * i + 2] = dl * a2 - ml; w[4 * i + 3] = dl * a3 - ml;
+            cvt4((qw[i] >> 4) & 0x0f0f0f0fu, a0, a1, a2, a3);
+            w[16 + 4 * i + 0] = dh * a0 - mh; w[16 + 4 * i + 1] = dh * a1 - mh;
+            w[16 + 4 * i + 2] = dh * a2 - mh; w[16 + 4 * i + 3] = dh * a3 - mh;
+        }
+    }
+};
+
+// Q6_K: all four 8-byte fields of a unit share the block's offset mod 4, so
+// each is kept as 3 aligned dwords plus one shift and funnel-shifted at decode.
+template <> struct RawUnits<T_Q6_K> {
+    uint32_t f[2][4][3];      // [hv][ql_lo, ql_hi, qh, scales][dwords]
+    uint32_t dw, sh;
+    __device__ __forceinline__ void load(const uint8_t *row, int s, int g)
+    {
+        const uint8_t *blk = row + (size_t)s * 210;
+        const uintptr_t a = (uintptr_t)blk;
+        sh = (uint32_t)(a & 3);
+        const uint8_t *base = (const uint8_t *)(a & ~(uintptr_t)3);
+#pragma unroll
+        for (int hv = 0; hv < 2; hv++) {
+            const int off[4] = { 64 * hv + 8 * g, 64 * hv + 32 + 8 * g, 128 + 32 * hv + 8 * g, 192 + 8 * hv };
+#pragma unroll
+            for (int fi = 0; fi < 4; fi++) {
+                const uint32_t *q = (const uint32_t *)(base + off[fi]);
+                f[hv][fi][0] = q[0]; f[hv][fi][1] = q[1]; f[hv][fi][2] = q[2];
+            }
+        }
+        dw = ld_u16(blk + 208);
+    }
+    // fragment t of unit (half hv, j = g): outputs 32t + 8g + i
+    __device__ __forceinline__ void decode_frags(int hv, int g, half8_t (&fr)[4]) const
+    {
+        uint32_t v[4][2];
+#pragma unroll
+        for (int fi = 0; fi < 4; fi++) {
+            v[fi][0] = __builtin_amdgcn_alignbyte(f[hv][fi][1], f[hv][fi][0], sh);
+            v[fi][1] = __builtin_amdgcn_alignbyte(f[hv][fi][2], f[hv][fi][1], sh);
+        }
+        const float d = h2f(dw);
+        const int s0 = g >> 1;
+        const uint32_t mg = vgpr_magic();
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float ds = d * (float)(int8_t)byte_of(t < 2 ? v[3][0] : v[3][1], (s0 + 2 * t) & 3);
+            const float cs = -1056.0f * ds;         // -(1024 + 32) * ds
+            _Float16 w[8];
+#pragma unroll
+            for (int ww = 0; ww < 2; ww++) {
+                const uint32_t ql = (t & 1) ? v[1][ww] : v[0][ww];
+                const uint32_t nib = (t < 2) ? ql : (ql >> 4);
+                const uint32_t hb = v[2][ww] >> (2 * t);
+                // code = nibble | (2 high bits << 4) per byte; bytes 0/2 and 1/3 feed the two fp16 lanes
+                const uint32_t code = (nib & 0x0f0f0f0fu) | ((hb & 0x03030303u) << 4);
+                fma4(code, code >> 8, 0x003f003fu, mg, ds, cs, w + 4 * ww);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) fr[t][i] = w[i];
+        }
+    }
+    __device__ __forceinline__ void decode(int hv, int g, float (&w)[32]) const
+    {
+        uint32_t v[4][2];
+#pragma unroll
+        for (int fi = 0; fi < 4; fi++) {
+            v[fi][0] = __builtin_amdgcn_alignbyte(f[hv][fi][1], f[hv][fi][0], sh);
+            v[fi][1] = __builtin_amdgcn_alignbyte(f[hv][fi][2], f[hv][fi][1], sh);
+        }
+        const float d = h2f(dw);
+        const int s0 = g >> 1;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float ds = d * (float)(int8_t)byte_of(t < 2 ? v[3][0] : v[3][1], (s0 + 2 * t) & 3);
+#pragma unroll
+            for (int ww = 0; ww < 2; ww++) {
+                const uint32_t ql = (t & 1) ? v[1][ww] : v[0][ww];
+                const uint32_t nib = (t < 2) ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
+                const uint32_t code = nib | (((v[2][ww] >> (2 * t)) & 0x03030303u) << 4);
+                float c0, c1, c2, c3;
+                cvt4(code, c0, c1, c2, c3);
+                w[8 * t + 4 * ww + 0] = ds * (c0 - 32.f); w[8 * t + 4 * ww + 1] = ds * (c1 - 32.f);
+                w[8 * t + 4 * ww + 2] = ds * (c2 - 32.f); w[8 * t + 4 * ww + 3] = ds * (c3 - 32.f);
+            }
+        }
+    }
+};
+
+// Q8_0: a 34-byte block at offset 0 or 2 mod 4 lies inside 9 aligned dwords.
+template <> struct RawUnits<T_Q8_0> {
+    uint32_t q[2][9];
+    uint32_t sh[2];
+    __device__ __forceinline__ void load(const uint8_t *row, int s, int g)
+    {
+#pragma unroll
+        for (int hv = 0; hv < 2; hv++) {
+            const uintptr_t a = (uintptr_t)(row + (size_t)(8 * s + g + 4 * hv) * 34);
+            sh[hv] = (uint32_t)(a & 3);
+            const uint32_t *p = (const uint32_t *)(a & ~(uintptr_t)3);
+#pragma unroll
+            for (int i = 0; i < 9; i++) q[hv][i] = p[i];
+        }
+    }
+    __device__ __forceinline__ void decode_frags(int hv, int g, half8_t (&fr)[4]) const
+    {
+        (void)g;
+        const bool al = sh[hv] == 0;
+        const float d = h2f(al ? (q[hv][0] & 0xffffu) : (q[hv][0] >> 16));
+        const float c = -1152.0f * d;               // codes stored as int8 + 128
+        const uint32_t mg = vgpr_magic();
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            _Float16 w[8];
+#pragma unroll
+            for (int dd = 0; dd < 2; dd++) {
+                const int i = 2 * p + dd;
+                const uint32_t x =
+                    (al ? __builtin_amdgcn_alignbyte(q[hv][i + 1], q[hv][i], 2) : q[hv][i + 1]) ^ 0x80808080u;
+                fma4(x, x >> 8, 0x00ff00ffu, mg, d, c, w + 4 * dd);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) fr[p][i] = w[i];
+        }
+    }
+    __device__ __forceinline__ void decode(int hv, int g, float (&w)[32]) const
+    {
+        (void)g;
+        const bool al = sh[hv] == 0;      // block starts on a dword: d low half, codes at byte 2
+        const float d = h2f(al ? (q[hv][0] & 0xffffu) : (q[hv][0] >> 16));
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t c = al ? __builtin_amdgcn_alignbyte(q[hv][i + 1], q[hv][i], 2) : q[hv][i + 1];
+#pragma unroll
+            for (int j = 0; j < 4; j++) w[4 * i + j] = (float)(int8_t)byte_of(c, j) * d;
+        }
+    }
+};
+
+// F32 rows: no register staging (64 floats per row would not fit); decode loads.
+template <> struct RawUnits<T_F32> {
+    const uint8_t *row;
+    int s;
+    __device__ __forceinline__ void load(const uint8_t *r, int ss, int g)
+    {
+        (void)g;
+        row = r;
+        s = ss;
+    }
+    __device__ __forceinline__ void decode(int hv, int g, float (&w)[32]) const
+    {
+        int k0[4];
+        unit_decode<T_F32>(row, 8 * s + g + 4 * hv, w, k0);
+    }
+    __device__ __forceinline__ void decode_frags(int hv, int g, half8_t (&fr)[4]) const
+    {
+        float w[32];
+        decode(hv, g, w);
+#pragma unroll
+        for (int p = 0; p < 4; p++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) fr[p][i] = (_Float16)w[8 * p + i];
+    }
+};
+
 // Sum over groups of G consecutive lanes (G a power of two <= 64); every lane
 // of the group ends with the group total.
 template <int G>

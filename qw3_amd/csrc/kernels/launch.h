@@ -35,7 +35,7 @@ bool gemv_type_ok(int type, int K);
 // x [T][K] and router rows (rtype, rw, rstride); wnorm2 [E] must then be set.
 // logits_out (may alias logits) receives the logits actually used.
 struct RouteArgs {
-    const float *logits;
+    const float *logits;       // [nparts][T][E] when nparts > 1 (part_stride floats apart)
     float *logits_out;
     int32_t *idx;
     float *scores;
@@ -50,8 +50,19 @@ struct RouteArgs {
     uint64_t rstride;
     const float *wnorm2;
     int32_t *guard_count;      // optional: number of tokens that took the exact recompute
+    int nparts = 1;
+    int64_t part_stride = 0;   // wnorm2 is then [nparts][E] as well
 };
 hipError_t launch_route(const RouteArgs &a, hipStream_t s);
+
+// Router logits on fp32 MFMA as nparts split-K partials: part[p][t][e];
+// wn[p][e] = sum of W[e][k]^2 over chunk p.  F32 / F16 / Q8_0 routers,
+// K % 64 == 0, E % 16 == 0, E <= 256, x rows 16-byte aligned, router rows
+// aligned for their element loads.
+bool router_mfma_ok(int rtype, int K, int E, const void *x, const void *rw, uint64_t rstride);
+int router_parts(int T, int K);
+hipError_t launch_router_logits(const float *x, int T, int K, int E, int rtype, const uint8_t *rw, uint64_t rstride,
+                                int nparts, float *part, float *wn, hipStream_t s);
 
 // Decode (small T) expert products.
 //   h[slot][F] = silu(x[t] . Wg_e) * (x[t] . Wu_e), slot = t*n_used + k, e = idx[slot]

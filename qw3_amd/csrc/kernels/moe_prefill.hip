@@ -9,14 +9,16 @@
 // where pos runs over expert e's compacted token positions.
 //
 // Precision: operands are fp16 (x, dequantised weights, h), accumulation is
-// fp32 in v_mfma_f32_16x16x32_f16.  Weights are dequantised exactly in fp32
-// and rounded once to fp16.
+// fp32 in v_mfma_f32_16x16x32_f16.  Each weight is one fp32-precision FMA on
+// its code rounded once to fp16.
 //
 // Work decomposition: blockIdx.y = work item (expert, 64-token tile) from the
-// bucketing kernel, blockIdx.x = 128-row output tile.  Each of the 4 waves
-// owns 32 output rows (2 MFMA column blocks; gate and up both for gate_up),
-// keeps their dequantised weight fragments in registers and applies them to
-// all 16-token row blocks of the tile, which sit in LDS as fp16.  Per 256-wide
+// bucketing kernel, blockIdx.x = 128-row output tile.  Each of the 8 waves
+// owns 16 output rows (one MFMA column block; for gate_up the same rows of
+// gate and up, so SwiGLU happens in registers), decodes their weight
+// fragments in registers (common.h RawUnits::decode_frags) and applies them
+// to all 16-token row blocks of the tile, which sit in LDS as fp16.  Weight
+// bytes of step s+1 load while step s computes.  Per 256-wide
 // K step, lane group g (lanes 16g..16g+15) holds units g and g+4 of its row
 // (see common.h); K-slot q of the step is segment q%4 of unit g+4*(q/4), and
 // the A fragment is read from the same K positions, so the MFMA's K order is a
@@ -30,9 +32,11 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int GM_TILE_M = 64;
-constexpr int GM_TPB = 256;
+constexpr int GM_WAVES = 8;
+constexpr int GM_TPB = GM_WAVES * 64;
 constexpr int GM_ROW = 256 + 8;           // halves per LDS row (16-byte pad)
-constexpr int GM_TILE_N = 128;
+constexpr int GM_TILE_N = 16 * GM_WAVES;  // output rows per workgroup (16 per wave)
+constexpr int GM_ACH = GM_TILE_M * 32 / GM_TPB;   // 16-byte A chunks per thread per K step
 
 template <int TYPE>
 __device__ __forceinline__ int slot_k0(int s, int g, int q)
@@ -46,30 +50,23 @@ __device__ __forceinline__ int slot_k0(int s, int g, int q)
         return 256 * s + 32 * c + 8 * part;
 }
 
-__device__ __forceinline__ half8 to_half8(const float *w)
-{
-    half8 r;
-#pragma unroll
-    for (int i = 0; i < 8; i++) r[i] = (_Float16)w[i];
-    return r;
-}
-
 __device__ __forceinline__ const uint8_t *ebase(const uint8_t *base, const uint64_t *table, int e, int which,
                                                 uint64_t rows, uint64_t stride)
 {
     return base + (table ? table[3 * e + which] : (uint64_t)e * rows * stride);
 }
 
-// Stage A rows [m][256 s .. 256 s + 255] of the tile: 64 rows x 32 chunks of
-// 16 bytes, 8 chunks per thread.  Rows beyond the tile are zero.
+// A tile of one K step: 64 rows x 32 chunks of 16 bytes (rows beyond the
+// tile are zero); thread covers rows (tid>>5) + (GM_TPB/32)*i, chunk tid&31.
 struct ATile {
-    uint4 r[8];
+    uint4 r[GM_ACH];
 };
 
-__device__ __forceinline__ void a_load(ATile &a, const _Float16 *src, const int64_t (&row_off)[8], int s, int chunk)
+__device__ __forceinline__ void a_load(ATile &a, const _Float16 *src, const int64_t (&row_off)[GM_ACH], int s,
+                                       int chunk)
 {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
+    for (int i = 0; i < GM_ACH; i++) {
         if (row_off[i] >= 0) a.r[i] = *(const uint4 *)(src + row_off[i] + 256 * s + 8 * chunk);
         else a.r[i] = make_uint4(0u, 0u, 0u, 0u);
     }
@@ -78,40 +75,85 @@ __device__ __forceinline__ void a_load(ATile &a, const _Float16 *src, const int6
 __device__ __forceinline__ void a_store(const ATile &a, _Float16 *As, int row0, int chunk)
 {
 #pragma unroll
-    for (int i = 0; i < 8; i++) *(uint4 *)(As + (row0 + 8 * i) * GM_ROW + 8 * chunk) = a.r[i];
+    for (int i = 0; i < GM_ACH; i++) *(uint4 *)(As + (row0 + (GM_TPB / 32) * i) * GM_ROW + 8 * chunk) = a.r[i];
 }
 
-// NB column blocks of 16 rows per wave; `pairs` = gate/up (NB = 4: g0 g1 u0 u1)
-// or down (NB = 2).
-template <int TYPE, int NB>
-__device__ __forceinline__ void gm_core(const _Float16 *As, const uint8_t *const (&rows)[NB], int s, int lane,
-                                        int mblocks, floatx4 (&acc)[4][NB])
+// One 256-wide K step for NB column blocks of 16 rows (gate/up: NB = 2,
+// gate and up of the same rows; down: NB = 1), weights from `raw`.
+template <int TYPE, int NB, int MB>
+__device__ __forceinline__ void gm_step(const _Float16 *As, const RawUnits<TYPE> (&raw)[NB], int s, int lane,
+                                        floatx4 (&acc)[4][NB])
 {
     const int g = lane >> 4, m = lane & 15;
 #pragma unroll
     for (int hv = 0; hv < 2; hv++) {
         half8 bq[NB][4];
 #pragma unroll
-        for (int nb = 0; nb < NB; nb++) {
-            float w[32];
-            int k0[4];
-            unit_decode<TYPE>(rows[nb], 8 * s + g + 4 * hv, w, k0);
-#pragma unroll
-            for (int p = 0; p < 4; p++) bq[nb][p] = to_half8(w + 8 * p);
-        }
+        for (int nb = 0; nb < NB; nb++) raw[nb].decode_frags(hv, g, bq[nb]);
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const int col = slot_k0<TYPE>(s, g, 4 * hv + p) - 256 * s;
 #pragma unroll
-            for (int mb = 0; mb < 4; mb++) {
-                if (mb < mblocks) {
-                    const half8 a = *(const half8 *)(As + (16 * mb + m) * GM_ROW + col);
+            for (int mb = 0; mb < MB; mb++) {
+                const half8 a = *(const half8 *)(As + (16 * mb + m) * GM_ROW + col);
 #pragma unroll
-                    for (int nb = 0; nb < NB; nb++)
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[nb][p], acc[mb][nb], 0, 0, 0);
-                }
+                for (int nb = 0; nb < NB; nb++)
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq[nb][p], acc[mb][nb], 0, 0, 0);
             }
         }
+    }
+}
+
+// One step of the K loop: publish the A tile of step s, start the loads of
+// step s+1 (A into registers, weights into `nxt`), then compute step s.
+template <int TYPE, int NB, int MB>
+__device__ __forceinline__ void gm_iter(const _Float16 *a_src, const int64_t (&row_off)[GM_ACH], int arow0,
+                                        int achunk, const uint8_t *const (&rows)[NB], int s, int S, int lane,
+                                        _Float16 *As, ATile &a, const RawUnits<TYPE> (&cur)[NB],
+                                        RawUnits<TYPE> (&nxt)[NB], floatx4 (&acc)[4][NB])
+{
+    __syncthreads();
+    a_store(a, As, arow0, achunk);
+    __syncthreads();
+    if (s + 1 < S) {
+        a_load(a, a_src, row_off, s + 1, achunk);
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) nxt[nb].load(rows[nb], s + 1, lane >> 4);
+    }
+    gm_step<TYPE, NB, MB>(As, cur, s, lane, acc);
+}
+
+// K loop shared by both kernels; two raw buffers alternate so staged weight
+// bytes are never copied.
+// MB = number of 16-token row blocks with data (1..4), a template parameter
+// so the MFMA sequence has no data-dependent branches.
+template <int TYPE, int NB, int MB>
+__device__ __forceinline__ void gm_kloop(const _Float16 *a_src, const int64_t (&row_off)[GM_ACH], int arow0, int achunk,
+                                         const uint8_t *const (&rows)[NB], int S, int lane,
+                                         _Float16 *As, floatx4 (&acc)[4][NB])
+{
+    ATile a;
+    a_load(a, a_src, row_off, 0, achunk);
+    RawUnits<TYPE> r0[NB], r1[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) r0[nb].load(rows[nb], 0, lane >> 4);
+    for (int s = 0; s < S; s += 2) {
+        gm_iter<TYPE, NB, MB>(a_src, row_off, arow0, achunk, rows, s, S, lane, As, a, r0, r1, acc);
+        if (s + 1 < S)
+            gm_iter<TYPE, NB, MB>(a_src, row_off, arow0, achunk, rows, s + 1, S, lane, As, a, r1, r0, acc);
+    }
+}
+
+template <int TYPE, int NB>
+__device__ __forceinline__ void gm_kloop_mb(int mblocks, const _Float16 *a_src, const int64_t (&row_off)[GM_ACH],
+                                            int arow0, int achunk, const uint8_t *const (&rows)[NB], int S, int lane,
+                                            _Float16 *As, floatx4 (&acc)[4][NB])
+{
+    switch (mblocks) {
+    case 1: gm_kloop<TYPE, NB, 1>(a_src, row_off, arow0, achunk, rows, S, lane, As, acc); break;
+    case 2: gm_kloop<TYPE, NB, 2>(a_src, row_off, arow0, achunk, rows, S, lane, As, acc); break;
+    case 3: gm_kloop<TYPE, NB, 3>(a_src, row_off, arow0, achunk, rows, S, lane, As, acc); break;
+    default: gm_kloop<TYPE, NB, 4>(a_src, row_off, arow0, achunk, rows, S, lane, As, acc); break;
     }
 }
 
@@ -131,37 +173,26 @@ k_grouped_gate_up(const _Float16 *__restrict__ x16, int K, ExpertWeights ew, int
     const int mblocks = (mrows + 15) / 16;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-    // A staging: thread covers rows (tid>>5) + 8i, 16-byte chunk tid&31.
     const int arow0 = tid >> 5, achunk = tid & 31;
-    int64_t row_off[8];
+    int64_t row_off[GM_ACH];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int r = arow0 + 8 * i;
+    for (int i = 0; i < GM_ACH; i++) {
+        const int r = arow0 + (GM_TPB / 32) * i;
         row_off[i] = r < mrows ? (int64_t)b.ids[off + m0 + r] * K : -1;
     }
 
     const uint8_t *wg = ebase(ew.gate, ew.table, e, 0, (uint64_t)F, ew.gate_stride);
     const uint8_t *wu = ebase(ew.up, ew.table, e, 1, (uint64_t)F, ew.up_stride);
-    const int nrow = blockIdx.x * GM_TILE_N + 32 * wave + (lane & 15);
-    const uint8_t *rows[4] = { wg + (size_t)nrow * ew.gate_stride, wg + (size_t)(nrow + 16) * ew.gate_stride,
-                               wu + (size_t)nrow * ew.up_stride, wu + (size_t)(nrow + 16) * ew.up_stride };
+    const int nrow = blockIdx.x * GM_TILE_N + 16 * wave + (lane & 15);
+    const uint8_t *rows[2] = { wg + (size_t)nrow * ew.gate_stride, wu + (size_t)nrow * ew.up_stride };
 
-    floatx4 acc[4][4];
+    floatx4 acc[4][2];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = floatx4{ 0.f, 0.f, 0.f, 0.f };
+        for (int j = 0; j < 2; j++) acc[i][j] = floatx4{ 0.f, 0.f, 0.f, 0.f };
 
-    const int S = K / 256;
-    ATile a;
-    a_load(a, x16, row_off, 0, achunk);
-    for (int s = 0; s < S; s++) {
-        __syncthreads();
-        a_store(a, As, arow0, achunk);
-        __syncthreads();
-        if (s + 1 < S) a_load(a, x16, row_off, s + 1, achunk);
-        gm_core<TYPE, 4>(As, rows, s, lane, mblocks, acc);
-    }
+    gm_kloop_mb<TYPE, 2>(mblocks, x16, row_off, arow0, achunk, rows, K / 256, lane, As, acc);
 
     // Epilogue: lane holds rows 4*(lane>>4)+j of each 16-row block, column lane&15.
 #pragma unroll
@@ -169,12 +200,8 @@ k_grouped_gate_up(const _Float16 *__restrict__ x16, int K, ExpertWeights ew, int
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int mr = 16 * mb + 4 * (lane >> 4) + j;
-            if (mr < mrows) {
-                _Float16 *dst = h16 + (int64_t)(off + m0 + mr) * F + nrow;
-#pragma unroll
-                for (int nb = 0; nb < 2; nb++)
-                    dst[16 * nb] = (_Float16)swiglu(acc[mb][nb][j], acc[mb][nb + 2][j]);
-            }
+            if (mr < mrows)
+                h16[(int64_t)(off + m0 + mr) * F + nrow] = (_Float16)swiglu(acc[mb][0][j], acc[mb][1][j]);
         }
     }
 }
@@ -196,44 +223,29 @@ k_grouped_down(const _Float16 *__restrict__ h16, int F, ExpertWeights ew, int N,
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
     const int arow0 = tid >> 5, achunk = tid & 31;
-    int64_t row_off[8];
+    int64_t row_off[GM_ACH];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int r = arow0 + 8 * i;
+    for (int i = 0; i < GM_ACH; i++) {
+        const int r = arow0 + (GM_TPB / 32) * i;
         row_off[i] = r < mrows ? (int64_t)(off + m0 + r) * F : -1;
     }
 
     const uint8_t *wd = ebase(ew.down, ew.table, e, 2, (uint64_t)N, ew.down_stride);
-    const int nrow = blockIdx.x * GM_TILE_N + 32 * wave + (lane & 15);
-    const uint8_t *rows[2] = { wd + (size_t)nrow * ew.down_stride, wd + (size_t)(nrow + 16) * ew.down_stride };
+    const int nrow = blockIdx.x * GM_TILE_N + 16 * wave + (lane & 15);
+    const uint8_t *rows[1] = { wd + (size_t)nrow * ew.down_stride };
 
-    floatx4 acc[4][2];
+    floatx4 acc[4][1];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = floatx4{ 0.f, 0.f, 0.f, 0.f };
+    for (int i = 0; i < 4; i++) acc[i][0] = floatx4{ 0.f, 0.f, 0.f, 0.f };
 
-    const int S = F / 256;
-    ATile a;
-    a_load(a, h16, row_off, 0, achunk);
-    for (int s = 0; s < S; s++) {
-        __syncthreads();
-        a_store(a, As, arow0, achunk);
-        __syncthreads();
-        if (s + 1 < S) a_load(a, h16, row_off, s + 1, achunk);
-        gm_core<TYPE, 2>(As, rows, s, lane, mblocks, acc);
-    }
+    gm_kloop_mb<TYPE, 1>(mblocks, h16, row_off, arow0, achunk, rows, F / 256, lane, As, acc);
 
 #pragma unroll
     for (int mb = 0; mb < 4; mb++) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int mr = 16 * mb + 4 * (lane >> 4) + j;
-            if (mr < mrows) {
-                float *dst = y + (int64_t)(off + m0 + mr) * N + nrow;
-#pragma unroll
-                for (int nb = 0; nb < 2; nb++) dst[16 * nb] = acc[mb][nb][j];
-            }
+            if (mr < mrows) y[(int64_t)(off + m0 + mr) * N + nrow] = acc[mb][0][j];
         }
     }
 }
