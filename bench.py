@@ -49,8 +49,12 @@ def parse():
     p.add_argument("--no-t1", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--cpu-tokens", type=int, default=512)
+    p.add_argument("--copy-mib", type=int, default=0,
+                   help="first run a plain device copy of this many MiB (k_copy, three times): the known-size "
+                        "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings")
     p.add_argument("--traffic", type=str, default=None,
-                   help="JSON {kernel: bytes_per_launch} measured by rocprofv3 --pmc (profiles/)")
+                   help="JSON {kernel: HBM bytes per launch} from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs "
+                        "(default: profiles/hbm_traffic.json)")
     return p.parse_args()
 
 
@@ -74,6 +78,9 @@ def kernel_bytes(name, spec, T, counts, n_used):
 
 
 def run_gpu(args, T, steps, warmup, layers, xs, spec, n_used=8):
+    """Warmup steps with every kernel timed (per-kernel breakdown, choice of
+    the dominant kernel), then the timed steps with only the dominant kernel
+    bracketed by events, so the other launches run back to back."""
     from qw3_amd import ds3
     from qw3_amd._native import hip
     E, K = spec.n_expert, spec.n_embd
@@ -86,13 +93,23 @@ def run_gpu(args, T, steps, warmup, layers, xs, spec, n_used=8):
         ds3.moe_ffn_batch(xs[i % len(xs)], d.router, spec.router_type, d.experts, out, T, E, n_used,
                           indices=idx if i == 0 else None)
 
+    step(0)                                   # first touch, routing histogram
+    hip().ds3_hip_synchronize()
+    counts = np.bincount(idx.read(np.int32, (T, n_used)).reshape(-1), minlength=E)
+    hip().ds3_hip_kernel_timing_only(None)
+    hip().ds3_hip_kernel_timing_reset()
+    hip().ds3_hip_kernel_timing(1)
     hip().ds3_hip_begin_batch()
-    for i in range(warmup):
+    for i in range(1, warmup + 1):
         step(i)
     hip().ds3_hip_end_batch()
-    counts = np.bincount(idx.read(np.int32, (T, n_used)).reshape(-1), minlength=E)
+    hip().ds3_hip_kernel_timing(0)
+    breakdown = ds3.kernel_stats()
+    dominant = max((k for k in breakdown if kernel_bytes(k, spec, T, counts, n_used) is not None),
+                   key=lambda k: breakdown[k][1])
     # timed region: synchronise, K steps enqueued back to back, synchronise
     hip().ds3_hip_kernel_timing_reset()
+    hip().ds3_hip_kernel_timing_only(dominant.encode())
     hip().ds3_hip_kernel_timing(1)
     hip().ds3_hip_synchronize()
     hip().ds3_hip_begin_batch()
@@ -104,13 +121,13 @@ def run_gpu(args, T, steps, warmup, layers, xs, spec, n_used=8):
     hip().ds3_hip_end_batch()
     wall_ms = (time.perf_counter() - t0) * 1e3
     hip().ds3_hip_kernel_timing(0)
+    hip().ds3_hip_kernel_timing_only(None)
     stats = ds3.kernel_stats()
-    return wall_ms, gpu_ms, stats, counts
+    return wall_ms, gpu_ms, stats, breakdown, counts
 
 
 def roofline(stats, spec, T, counts, n_used, traffic):
-    name = max((k for k in stats if kernel_bytes(k, spec, T, counts, n_used) is not None),
-               key=lambda k: stats[k][1])
+    name = next(iter(stats))                  # the one kernel timed in the timed region
     n, ms = stats[name]
     avg_s = ms / n / 1e3
     b = kernel_bytes(name, spec, T, counts, n_used)
@@ -121,6 +138,14 @@ def roofline(stats, spec, T, counts, n_used, traffic):
     if traffic and name in traffic:
         r["traffic"] = traffic[name]
     return r
+
+
+def log_breakdown(brk, stats):
+    log("[bench]   warmup, every kernel bracketed by events:")
+    for k, (n, ms) in sorted(brk.items(), key=lambda kv: -kv[1][1]):
+        log(f"[bench]     {k:24s} {n:5d} launches  avg {ms / n * 1e3:8.2f} us")
+    for k, (n, ms) in stats.items():
+        log(f"[bench]   timed region, {k} alone: {n} launches avg {ms / n * 1e3:.2f} us")
 
 
 def cpu_baseline(layer, x, n_used, n_tokens):
@@ -174,6 +199,17 @@ def main():
     ds3.init()
     info = ds3.device_info()
     log(f"[bench] device {info['arch']} CUs={info['n_cu']}")
+    if args.copy_mib:
+        from qw3_amd._native import hip
+        n = args.copy_mib << 20
+        a, b = ds3.Buffer.alloc(n), ds3.Buffer.alloc(n)
+        for _ in range(3):
+            if hip().ds3_hip_buffer_copy_f32(a, b, n) != 0:
+                raise RuntimeError("buffer_copy_f32 failed")
+        hip().ds3_hip_synchronize()
+        log(f"[bench] copy calibration: 3 x {args.copy_mib} MiB device copy")
+        a.close()
+        b.close()
     spec = W.config_spec(args.config)
     T, n_used = args.tokens, W.N_USED
     t0 = time.perf_counter()
@@ -187,12 +223,12 @@ def main():
     xs_host = [W.make_inputs(args.config, T, seed=99, step=s) for s in range(4)]
     xs = [ds3.Buffer.from_array(x) for x in xs_host]
 
-    wall_ms, gpu_ms, stats, counts = run_gpu(args, T, args.steps, args.warmup, layers, xs, spec, n_used)
+    wall_ms, gpu_ms, stats, brk, counts = run_gpu(args, T, args.steps, args.warmup, layers, xs, spec, n_used)
     ms_step = wall_ms / args.steps
     log(f"[bench] T={T}: {ms_step * 1e3:.1f} us/step wall, {gpu_ms / args.steps * 1e3:.1f} us/step events")
-    for k, (n, ms) in sorted(stats.items(), key=lambda kv: -kv[1][1]):
-        log(f"[bench]   {k:24s} {n:5d} launches  avg {ms / n * 1e3:8.2f} us")
-    traffic = json.loads(Path(args.traffic).read_text()) if args.traffic else None
+    log_breakdown(brk, stats)
+    tpath = Path(args.traffic) if args.traffic else ROOT / "profiles" / "hbm_traffic.json"
+    traffic = json.loads(tpath.read_text()) if tpath.exists() else None
     rl = roofline(stats, spec, T, counts, n_used, traffic)
     flops = W.algorithmic_flops(spec, T, n_used)
     line = {
@@ -225,11 +261,10 @@ def main():
         layers1 = layers if args.config in (1, 2) else [W.make_layer(spec1, seed=1234, layer=l).to_device()
                                                         for l in range(args.layers)]
         x1 = [ds3.Buffer.from_array(W.make_inputs(1, 1, seed=98, step=s)) for s in range(16)]
-        w1, g1, st1, c1 = run_gpu(args, 1, args.t1_steps, args.warmup, layers1, x1, spec1, n_used)
+        w1, g1, st1, brk1, c1 = run_gpu(args, 1, args.t1_steps, args.warmup, layers1, x1, spec1, n_used)
         ms1 = w1 / args.t1_steps
-        log(f"[bench] T=1: {ms1 * 1e3:.1f} us/step wall")
-        for k, (n, ms) in sorted(st1.items(), key=lambda kv: -kv[1][1]):
-            log(f"[bench]   {k:24s} {n:5d} launches  avg {ms / n * 1e3:8.2f} us")
+        log(f"[bench] T=1: {ms1 * 1e3:.1f} us/step wall, {g1 / args.t1_steps * 1e3:.1f} us/step events")
+        log_breakdown(brk1, st1)
         b1 = W.algorithmic_bytes(spec1, 1, n_used)
         line["t1"] = {"value": round(1 / (ms1 / 1e3), 1), "unit": "tokens/s", "ms_per_step": round(ms1, 5),
                       "steps": args.t1_steps, "alg_bytes_per_step": b1,

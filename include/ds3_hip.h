@@ -241,6 +241,10 @@ int64_t ds3_hip_guard_count(void);
  * synchronises and reports, for kernel i (0-based; returns -1 past the end),
  * its name, launch count and summed duration in milliseconds. */
 void ds3_hip_kernel_timing(int enable);
+/* Restrict kernel timing to launches of the kernel called `name` (NULL or ""
+ * restores timing of every kernel), so that one kernel can be timed without
+ * event pairs between the others. */
+void ds3_hip_kernel_timing_only(const char *name);
 void ds3_hip_kernel_timing_reset(void);
 int  ds3_hip_kernel_stats(int i, char *name, size_t name_len, int64_t *count, double *total_ms);
 

@@ -53,6 +53,7 @@ struct State {
     hipEvent_t bev0 = nullptr, bev1 = nullptr;
     // per-kernel timing
     bool ktiming = false;
+    std::string ktiming_only;          // empty: every kernel
     std::vector<hipEvent_t> pool;
     int pool_used = 0;
     std::vector<KRec> recs;
@@ -128,7 +129,7 @@ struct KScope {
     const char *name;
     explicit KScope(const char *n) : name(n)
     {
-        if (g.ktiming && g.pool_used + 2 <= (int)g.pool.size()) {
+        if (g.ktiming && g.pool_used + 2 <= (int)g.pool.size() && (g.ktiming_only.empty() || g.ktiming_only == n)) {
             e0 = g.pool_used;
             g.pool_used += 2;
             (void)hipEventRecord(g.pool[e0], g.stream);
@@ -587,39 +588,67 @@ struct RouteBufs {
     float *logits;       // [T][E] logits actually used (output)
     int32_t *idx;
     float *scores;
-    float *wnorm2;       // [nparts][E] scratch
-    float *part;         // [nparts][T][E] scratch (MFMA router)
+    float *part;         // [nparts][T][E] split-K partial logits (MFMA router)
+    float *wmax;         // [nparts] per-chunk max row sum of squares (MFMA router)
+    float *xsq;          // [nparts][T] per-chunk sum of x^2 (MFMA router)
+    float *wn_rows;      // [E] row sums of squares (GEMV router)
+    _Float16 *x16;       // optional [T][n_embd] fp16 copy of x, written by the MFMA router
 };
 
-// Scratch of route_tokens beyond the output buffers.
-size_t route_scratch_bytes(int T, uint32_t n_embd, uint32_t n_expert)
+// Scratch of route_tokens beyond the output buffers, laid out from `base`.
+struct RouteScratch {
+    size_t o_part, o_wmax, o_xsq, o_wn, bytes;
+};
+
+RouteScratch route_scratch(int T, uint32_t n_embd, uint32_t n_expert)
 {
     const int np = router_parts(T, (int)n_embd);
-    return ((size_t)np * n_expert * 4 + 255) / 256 * 256 + (size_t)np * T * n_expert * 4;
+    Bump b;
+    RouteScratch r;
+    r.o_part = b.take((size_t)np * T * n_expert * 4);
+    r.o_wmax = b.take((size_t)np * 4);
+    r.o_xsq = b.take((size_t)np * T * 4);
+    r.o_wn = b.take((size_t)n_expert * 4);
+    r.bytes = b.off;
+    return r;
 }
 
+RouteBufs route_bufs(uint8_t *base, const RouteScratch &r, float *logits, int32_t *idx, float *scores,
+                     _Float16 *x16)
+{
+    return RouteBufs{ logits, idx, scores, (float *)(base + r.o_part), (float *)(base + r.o_wmax),
+                      (float *)(base + r.o_xsq), (float *)(base + r.o_wn), x16 };
+}
+
+// Router logits + softmax/top-k/renorm for T tokens.  Returns 1 in *x16_done
+// when the MFMA router also wrote rb.x16.
 int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstride, int rtype, int T, uint32_t n_embd,
-                 uint32_t n_expert, uint32_t n_used, bool norm, const RouteBufs &rb)
+                 uint32_t n_expert, uint32_t n_used, bool norm, const RouteBufs &rb, bool *x16_done = nullptr)
 {
     hipError_t e;
     RouteArgs ra{};
+    if (x16_done) *x16_done = false;
     if (router_mfma_ok(rtype, (int)n_embd, (int)n_expert, x, cptr(router), rstride)) {
         const int np = router_parts(T, (int)n_embd);
         {
             KScope ks("router_logits");
             e = launch_router_logits(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, np, rb.part,
-                                     rb.wnorm2, g.stream);
+                                     rb.wmax, rb.xsq, rb.x16, g.stream);
         }
         ra.logits = rb.part;
         ra.nparts = np;
         ra.part_stride = (int64_t)T * n_expert;
         ra.logits_out = rb.logits;
+        ra.wmax_parts = rb.wmax;
+        ra.xsq_parts = rb.xsq;
+        if (x16_done) *x16_done = rb.x16 != nullptr;
     } else {
         KScope ks("router_logits");
         e = launch_gemv(rtype, x, n_embd, cptr(router), rstride, rb.logits, n_expert, T, (int)n_expert, (int)n_embd,
-                        rb.wnorm2, g.stream);
+                        rb.wn_rows, g.stream);
         ra.logits = rb.logits;
         ra.logits_out = nullptr;
+        ra.wn_rows = rb.wn_rows;
     }
     if (e != hipSuccess) return report(e, "router logits");
     ra.idx = rb.idx;
@@ -635,7 +664,6 @@ int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstrid
     ra.rtype = rtype;
     ra.rw = cptr(router);
     ra.rstride = rstride;
-    ra.wnorm2 = rb.wnorm2;
     ra.guard_count = g.guard;
     KScope ks("router_topk");
     return report(launch_route(ra, g.stream), "router topk");
@@ -696,16 +724,15 @@ extern "C" int ds3_hip_moe_ffn(
     const uint32_t ff_max = has_shared && n_ff_shared > n_ff_exp ? n_ff_shared : n_ff_exp;
     Bump bp;
     const size_t o_idx = bp.take((size_t)n_used * 4), o_sc = bp.take((size_t)n_used * 4);
-    const size_t o_r = bp.take(route_scratch_bytes(1, n_embd, n_expert));
+    const RouteScratch rs = route_scratch(1, n_embd, n_expert);
+    const size_t o_r = bp.take(rs.bytes);
     const size_t o_h = bp.take((size_t)n_used * ff_max * 4), o_t = bp.take((size_t)n_used * ff_max * 4);
     uint8_t *ws = ws_get(bp.off);
     if (!ws) return -1;
     int32_t *idx = (int32_t *)(ws + o_idx);
     float *sc = (float *)(ws + o_sc), *h = (float *)(ws + o_h), *tmp = (float *)(ws + o_t);
     const float *x = fptr(input);
-    const int np = router_parts(1, (int)n_embd);
-    RouteBufs rb{ fptr(gate_logits), idx, sc, (float *)(ws + o_r),
-                  (float *)(ws + o_r + ((size_t)np * n_expert * 4 + 255) / 256 * 256) };
+    const RouteBufs rb = route_bufs(ws + o_r, rs, fptr(gate_logits), idx, sc, nullptr);
     if (route_tokens(x, w_gate_inp, router_row_stride, router_type, 1, n_embd, n_expert, n_used, norm_topk_prob,
                      rb) != 0)
         return -1;
@@ -853,12 +880,12 @@ extern "C" int ds3_hip_moe_route(const ds3_hip_buffer_t *input, const ds3_hip_bu
         !fits(scores, T * n_used * 4, "scores") || !fits(gate_logits, T * n_expert * 4, "gate_logits"))
         return -1;
     Bump bp;
-    const size_t o_l = bp.take(T * n_expert * 4), o_r = bp.take(route_scratch_bytes((int)T, n_embd, n_expert));
+    const RouteScratch rs = route_scratch((int)T, n_embd, n_expert);
+    const size_t o_l = bp.take(T * n_expert * 4), o_r = bp.take(rs.bytes);
     uint8_t *ws = ws_get(bp.off);
     if (!ws) return -1;
-    const int np = router_parts((int)T, (int)n_embd);
-    RouteBufs rb{ gate_logits ? fptr(gate_logits) : (float *)(ws + o_l), (int32_t *)dptr(indices), fptr(scores),
-                  (float *)(ws + o_r), (float *)(ws + o_r + ((size_t)np * n_expert * 4 + 255) / 256 * 256) };
+    const RouteBufs rb = route_bufs(ws + o_r, rs, gate_logits ? fptr(gate_logits) : (float *)(ws + o_l),
+                                    (int32_t *)dptr(indices), fptr(scores), nullptr);
     if (route_tokens(fptr(input), w_gate_inp, router_row_stride, router_type, (int)T, n_embd, n_expert, n_used,
                      norm_topk_prob, rb) != 0)
         return -1;
@@ -927,12 +954,12 @@ extern "C" int ds3_hip_moe_ffn_batch(
 
     Bump bp;
     const size_t o_l = bp.take(T * n_expert * 4), o_i = bp.take(T * n_used * 4), o_s = bp.take(T * n_used * 4);
-    const size_t o_w = bp.take(route_scratch_bytes((int)T, n_embd, n_expert));
-    const int np = router_parts((int)T, (int)n_embd);
+    const RouteScratch rs = route_scratch((int)T, n_embd, n_expert);
+    const size_t o_w = bp.take(rs.bytes);
     size_t o_h = 0, o_t = 0, o_x16 = 0, o_cnt = 0, o_off = 0, o_ids = 0, o_wts = 0, o_pos = 0, o_tiles = 0, o_nt = 0,
            o_h16 = 0, o_y = 0;
     if (use_grouped) {
-        o_x16 = bp.take(Tc * n_embd * 2);
+        o_x16 = bp.take(T * n_embd * 2);
         o_cnt = bp.take((size_t)n_expert * 4);
         o_off = bp.take(((size_t)n_expert + 1) * 4);
         o_ids = bp.take(S * 4);
@@ -948,13 +975,14 @@ extern "C" int ds3_hip_moe_ffn_batch(
     }
     uint8_t *ws = ws_get(bp.off);
     if (!ws) return -1;
-    RouteBufs rb{ gate_logits ? fptr(gate_logits) : (float *)(ws + o_l),
-                  indices ? (int32_t *)dptr(indices) : (int32_t *)(ws + o_i),
-                  scores ? fptr(scores) : (float *)(ws + o_s), (float *)(ws + o_w),
-                  (float *)(ws + o_w + ((size_t)np * n_expert * 4 + 255) / 256 * 256) };
+    const RouteBufs rb = route_bufs(ws + o_w, rs, gate_logits ? fptr(gate_logits) : (float *)(ws + o_l),
+                                    indices ? (int32_t *)dptr(indices) : (int32_t *)(ws + o_i),
+                                    scores ? fptr(scores) : (float *)(ws + o_s),
+                                    use_grouped ? (_Float16 *)(ws + o_x16) : nullptr);
     const float *x = fptr(input);
+    bool x16_done = false;
     if (route_tokens(x, w_gate_inp, router_row_stride, router_type, (int)T, n_embd, n_expert, n_used, norm_topk_prob,
-                     rb) != 0)
+                     rb, &x16_done) != 0)
         return -1;
     ExpertWeights ew = make_ew(w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type, down_type, gate_row_stride,
                                up_row_stride, down_row_stride, expert_offsets);
@@ -968,17 +996,18 @@ extern "C" int ds3_hip_moe_ffn_batch(
     }
     BucketOut bo{ (int32_t *)(ws + o_cnt), (int32_t *)(ws + o_off), (int32_t *)(ws + o_ids), (float *)(ws + o_wts),
                   (int32_t *)(ws + o_pos), (int32_t *)(ws + o_tiles), (int32_t *)(ws + o_nt), max_tiles, 64 };
-    _Float16 *x16 = (_Float16 *)(ws + o_x16), *h16 = (_Float16 *)(ws + o_h16);
+    _Float16 *x16_all = (_Float16 *)(ws + o_x16), *h16 = (_Float16 *)(ws + o_h16);
     float *y = (float *)(ws + o_y);
+    if (!x16_done) {
+        KScope ks("to_f16");
+        const hipError_t e = launch_to_f16(x, x16_all, (int64_t)T * n_embd, g.stream);
+        if (e != hipSuccess) return report(e, "moe_ffn_batch to_f16");
+    }
     for (size_t t0 = 0; t0 < T; t0 += Tc) {
         const int tc = (int)((T - t0) < Tc ? (T - t0) : Tc);
-        const float *xc = x + t0 * n_embd;
-        hipError_t e;
+        const _Float16 *x16 = x16_all + t0 * n_embd;
+        hipError_t e = hipSuccess;
         {
-            KScope ks("to_f16");
-            e = launch_to_f16(xc, x16, (int64_t)tc * n_embd, g.stream);
-        }
-        if (e == hipSuccess) {
             KScope ks("bucket");
             e = launch_bucket(rb.idx + t0 * n_used, rb.scores + t0 * n_used, tc, (int)n_used, (int)n_expert, bo,
                               g.stream);
@@ -1105,6 +1134,11 @@ extern "C" void ds3_hip_kernel_timing(int enable)
         for (auto &e : g.pool) (void)hipEventCreate(&e);
     }
     g.ktiming = enable != 0;
+}
+
+extern "C" void ds3_hip_kernel_timing_only(const char *name)
+{
+    g.ktiming_only = name ? name : "";
 }
 
 extern "C" void ds3_hip_kernel_timing_reset(void)

@@ -21,6 +21,32 @@ namespace ds3k {
 constexpr int BUCKET_TPB = 1024;
 constexpr size_t BUCKET_LDS_BYTES = 60 * 1024;   // masks (u32) + prefix (u16)
 
+// Exclusive prefix sums of (a, b) over the workgroup's threads in thread
+// order; totals returned in ta, tb.
+__device__ __forceinline__ void block_scan2(int &a, int &b, int &ta, int &tb, int2 *wsum)
+{
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    int ia = a, ib = b;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const int ua = __shfl_up(ia, o, WAVE), ub = __shfl_up(ib, o, WAVE);
+        if (lane >= o) { ia += ua; ib += ub; }
+    }
+    if (lane == WAVE - 1) wsum[wave] = make_int2(ia, ib);
+    __syncthreads();
+    int pa = 0, pb = 0;
+    ta = 0;
+    tb = 0;
+    for (int w = 0; w < BUCKET_TPB / WAVE; w++) {
+        const int2 v = wsum[w];
+        if (w < wave) { pa += v.x; pb += v.y; }
+        ta += v.x;
+        tb += v.y;
+    }
+    a = pa + ia - a;
+    b = pb + ib - b;
+}
+
 __global__ void __launch_bounds__(BUCKET_TPB)
 k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int T, int k, int E, BucketOut o)
 {
@@ -28,7 +54,8 @@ k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int 
     const int chunks = (T + 31) / 32;
     uint32_t *mask = sm;                                  // [chunks][E]
     uint16_t *pre = (uint16_t *)(sm + chunks * E);        // [chunks][E] exclusive prefix
-    __shared__ int32_t off_s[1025];
+    __shared__ int32_t off_s[BUCKET_TPB];
+    __shared__ int2 wsum[BUCKET_TPB / WAVE];
     const int S = T * k;
     for (int i = threadIdx.x; i < chunks * E; i += BUCKET_TPB) mask[i] = 0u;
     __syncthreads();
@@ -37,40 +64,38 @@ k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int 
         if (e >= 0 && e < E) atomicOr(&mask[(t >> 5) * E + e], 1u << (t & 31));
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < E; e += BUCKET_TPB) {
-        int run = 0;
+    // thread e: its expert's per-chunk prefix, count and work items
+    const int e = threadIdx.x;                            // E <= BUCKET_TPB
+    int cnt = 0;
+    if (e < E) {
         for (int c = 0; c < chunks; c++) {
-            pre[c * E + e] = (uint16_t)run;
-            run += __popc(mask[c * E + e]);
+            pre[c * E + e] = (uint16_t)cnt;
+            cnt += __popc(mask[c * E + e]);
         }
-        o.counts[e] = run;
-        off_s[e] = run;
     }
-    __syncthreads();
+    int off = cnt, tb = (cnt + o.tile_m - 1) / o.tile_m, total = 0, total_t = 0;
+    const int ntile = tb;
+    block_scan2(off, tb, total, total_t, wsum);
+    if (e < E) {
+        o.counts[e] = cnt;
+        o.offsets[e] = off;
+        off_s[e] = off;
+        for (int m = 0; m < ntile && tb + m < o.max_tiles; m++) o.tiles[tb + m] = (e << 16) | m;
+    }
     if (threadIdx.x == 0) {
-        int run = 0, nt = 0;
-        for (int e = 0; e < E; e++) {
-            const int c = off_s[e];
-            off_s[e] = run;
-            o.offsets[e] = run;
-            for (int m = 0; m * o.tile_m < c; m++)
-                if (nt < o.max_tiles) o.tiles[nt++] = (e << 16) | m;
-            run += c;
-        }
-        off_s[E] = run;
-        o.offsets[E] = run;
-        *o.n_tiles = nt;
+        o.offsets[E] = total;
+        *o.n_tiles = total_t < o.max_tiles ? total_t : o.max_tiles;
     }
     __syncthreads();
     for (int s = threadIdx.x; s < S; s += BUCKET_TPB) {
-        const int t = s / k, e = idx[s];
-        if (e < 0 || e >= E) {            // out-of-range id: the slot is dropped
+        const int t = s / k, ex = idx[s];
+        if (ex < 0 || ex >= E) {          // out-of-range id: the slot is dropped
             o.slot_pos[s] = -1;
             continue;
         }
-        const int w = (t >> 5) * E + e;
+        const int w = (t >> 5) * E + ex;
         const int rank = (int)pre[w] + __popc(mask[w] & ((1u << (t & 31)) - 1u));
-        const int pos = off_s[e] + rank;
+        const int pos = off_s[ex] + rank;
         o.ids[pos] = t;
         o.wts[pos] = scores[s];
         o.slot_pos[s] = pos;

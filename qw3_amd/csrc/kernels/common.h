@@ -281,6 +281,7 @@ __device__ __forceinline__ void unit_decode(const uint8_t *row, int u, float (&w
 // ---------------------------------------------------------------------------
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 
 // 0x64006400 in a VGPR: with the mask in an SGPR, (x & mask) | magic is then
 // a single v_and_or_b32 (gfx9 VOP3 takes no literal and one SGPR).

@@ -80,22 +80,36 @@ __global__ void k_to_f16(const float *x, _Float16 *y, int64_t n4)
 }
 
 // out[t][j] = (acc ? out[t][j] : 0) + w_0 y[p_0][j] + ... in k order, then + residual.
+// Four consecutive columns per thread when N % 4 == 0 (VEC = 4), else one.
+template <int VEC>
 __global__ void k_combine(const float *__restrict__ y, const int32_t *__restrict__ slot_pos,
                           const float *__restrict__ wts, int k, int N, float *__restrict__ out, int64_t ldo,
                           const float *__restrict__ residual, int accumulate)
 {
 #pragma clang fp contract(off)
+    typedef float vec_t __attribute__((ext_vector_type(VEC)));
     const int t = blockIdx.y;
-    const int j = blockIdx.x * EW_TPB + threadIdx.x;
+    const int j = (blockIdx.x * EW_TPB + threadIdx.x) * VEC;
     if (j >= N) return;
+    constexpr int KMAX = 16;                  // slots whose loads are issued together
     float *o = out + (int64_t)t * ldo + j;
-    float acc = accumulate ? *o : 0.0f;
-    for (int kk = 0; kk < k; kk++) {
-        const int p = slot_pos[t * k + kk];
-        if (p >= 0) acc = acc + wts[t * k + kk] * y[(int64_t)p * N + j];
+    vec_t acc = accumulate ? *(const vec_t *)o : (vec_t)0.0f;
+    for (int k0 = 0; k0 < k; k0 += KMAX) {
+        vec_t v[KMAX];
+        float w[KMAX];
+        int p[KMAX];
+#pragma unroll
+        for (int kk = 0; kk < KMAX; kk++) {
+            p[kk] = k0 + kk < k ? slot_pos[t * k + k0 + kk] : -1;
+            w[kk] = p[kk] >= 0 ? wts[t * k + k0 + kk] : 0.0f;
+            v[kk] = p[kk] >= 0 ? *(const vec_t *)(y + (int64_t)p[kk] * N + j) : (vec_t)0.0f;
+        }
+#pragma unroll
+        for (int kk = 0; kk < KMAX; kk++)
+            if (p[kk] >= 0) acc = acc + w[kk] * v[kk];          // dropped slots add nothing
     }
-    if (residual) acc = acc + residual[(int64_t)t * ldo + j];
-    *o = acc;
+    if (residual) acc = acc + *(const vec_t *)(residual + (int64_t)t * ldo + j);
+    *(vec_t *)o = acc;
 }
 
 hipError_t launch_fill_zero(float *p, int64_t n, hipStream_t s)
@@ -154,9 +168,17 @@ hipError_t launch_to_f16(const float *x, _Float16 *y, int64_t n, hipStream_t s)
 hipError_t launch_combine(const float *y, const int32_t *slot_pos, const float *wts, int T, int k, int N, float *out,
                           int64_t ldo, const float *residual, bool accumulate, hipStream_t s)
 {
-    const dim3 grid((unsigned)((N + EW_TPB - 1) / EW_TPB), (unsigned)T);
-    hipLaunchKernelGGL(k_combine, grid, dim3(EW_TPB), 0, s, y, slot_pos, wts, k, N, out, ldo, residual,
-                       accumulate ? 1 : 0);
+    const bool vec4 = N % 4 == 0 && ldo % 4 == 0 &&
+                      ((((uintptr_t)y) | ((uintptr_t)out) | ((uintptr_t)residual)) & 15) == 0;
+    if (vec4) {
+        const dim3 grid((unsigned)((N / 4 + EW_TPB - 1) / EW_TPB), (unsigned)T);
+        hipLaunchKernelGGL(k_combine<4>, grid, dim3(EW_TPB), 0, s, y, slot_pos, wts, k, N, out, ldo, residual,
+                           accumulate ? 1 : 0);
+    } else {
+        const dim3 grid((unsigned)((N + EW_TPB - 1) / EW_TPB), (unsigned)T);
+        hipLaunchKernelGGL(k_combine<1>, grid, dim3(EW_TPB), 0, s, y, slot_pos, wts, k, N, out, ldo, residual,
+                           accumulate ? 1 : 0);
+    }
     return hipGetLastError();
 }
 

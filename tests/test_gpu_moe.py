@@ -101,6 +101,65 @@ def test_route_guard_resolves_near_ties(hip_ready):
     assert index_mismatches(gi, oi, probs) == 0
 
 
+def _near_tie_router(type_: int, E: int, K: int, rng):
+    """Router bytes whose rows 3 and 5 copy row 0 except one weight, moved by
+    one code (F32: by 1e-8 per element).  Returns (raw bytes, FP32 rows as the
+    oracle dequantises them, index of the changed weight)."""
+    if type_ == ds3.TYPE_F32:
+        wr = (rng.standard_normal((E, K)) * 0.02).astype(np.float32)
+        wr[3] = wr[0] + np.float32(1e-8)
+        wr[5] = wr[0] - np.float32(1.5e-8)
+        return wr.reshape(-1).view(np.uint8).copy(), wr, None
+    raw = W.quant_matrix(type_, W.NORMAL, 4321, 7, E, K, 0.0, 0.02).reshape(E, -1).copy()
+    raw[3] = raw[0]
+    raw[5] = raw[0]
+    blk = 1                                   # second block of the row
+    if type_ == ds3.TYPE_Q8_0:
+        b, j = 34 * blk + 2 + 5, 32 * blk + 5
+        for r, dq in ((3, 1), (5, -1)):
+            q = int(raw[r, b].astype(np.int8))
+            raw[r, b] = np.uint8(np.int8(q + dq if -127 < q + dq < 127 else q - dq))
+    elif type_ == ds3.TYPE_Q4_K:
+        b, j = 144 * blk + 16 + 32 * 1 + 7, 256 * blk + 64 + 7      # low nibble: weight 64*grp + l
+        for r in (3, 5):
+            n = int(raw[r, b]) & 15
+            raw[r, b] = (int(raw[r, b]) & 0xF0) | (n + 1 if n < 15 else n - 1)
+    else:                                     # Q6_K: ql[l] low nibble is weight 128h + l, h = 0
+        b, j = 210 * blk + 9, 256 * blk + 9
+        for r in (3, 5):
+            n = int(raw[r, b]) & 15
+            raw[r, b] = (int(raw[r, b]) & 0xF0) | (n + 1 if n < 15 else n - 1)
+    raw = raw.reshape(-1)
+    wr = O.dequantize(type_, raw, E * K).reshape(E, K)
+    return raw, wr, j
+
+
+@pytest.mark.parametrize("type_,E", [(ds3.TYPE_F32, 24), (ds3.TYPE_Q8_0, 16), (ds3.TYPE_Q8_0, 24),
+                                     (ds3.TYPE_Q4_K, 16), (ds3.TYPE_Q6_K, 16)])
+def test_route_guard_router_types(hip_ready, type_, E):
+    """Near ties on every router type and on both router paths (fp32 MFMA
+    logits for E % 16 == 0 with F32/F16/Q8_0 rows, the GEMV kernel
+    otherwise): the guard's exact recompute decodes each weight as the
+    reference's FP32 copy holds it, so selection matches the oracle."""
+    K, T, k = 2048, 64, 4
+    rng = np.random.default_rng(9)
+    raw, wr, j = _near_tie_router(type_, E, K, rng)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    if j is not None:
+        x[:, j] = np.float32(1e-3)            # one code step of that weight moves the logit ~1e-7
+    router = ds3.Buffer.from_array(raw)
+    before = ds3.guard_count()
+    xb = ds3.Buffer.from_array(x)
+    ib, sb = ds3.Buffer.alloc(T * k * 4), ds3.Buffer.alloc(T * k * 4)
+    ds3.moe_route(xb, router, type_, T, K, E, k, ib, sb)
+    gi = ib.read(np.int32, (T, k))
+    oi, _, probs = oracle_route(wr, x, k)
+    fired = ds3.guard_count() - before
+    print(f"    {ds3.TYPE_NAMES[type_]} E={E}: guard fired for {fired} of {T} tokens", flush=True)
+    assert fired > 0
+    assert index_mismatches(gi, oi, probs) == 0
+
+
 def test_topk_batch_entry_points(hip_ready):
     rng = np.random.default_rng(11)
     L, T, E, k = 3, 5, 128, 8
