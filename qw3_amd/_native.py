@@ -7,6 +7,7 @@ from qw3_amd/lib/.  Loading fails loudly: there is no CPU fallback.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
 LIB_DIR = Path(__file__).resolve().parent / "lib"
@@ -95,7 +96,8 @@ def hip() -> C.CDLL:
     """The HIP backend (libds3_hip.so).  Raises if it was not built."""
     global _hip
     if _hip is None:
-        path = LIB_DIR / "libds3_hip.so"
+        # DS3_HIP_LIB selects another build of the same library (tuning runs)
+        path = Path(os.environ.get("DS3_HIP_LIB", LIB_DIR / "libds3_hip.so"))
         if not path.exists():
             raise RuntimeError(f"{path} is missing: run python -c 'import __graft_entry__ as g; g.build()' "
                                "(there is no CPU fallback)")

@@ -243,7 +243,8 @@ extern "C" int ds3_hip_init(void)
     const float one = 1.0f;
     (void)hipMemcpy(g.zero_idx, &zi, sizeof zi, hipMemcpyHostToDevice);
     (void)hipMemcpy(g.one_f, &one, sizeof one, hipMemcpyHostToDevice);
-    (void)hipMemset(g.guard, 0, sizeof(int32_t));
+    (void)hipMemsetAsync(g.guard, 0, sizeof(int32_t), g.stream);
+    (void)hipStreamSynchronize(g.stream);
     (void)hipEventCreate(&g.bev0);
     (void)hipEventCreate(&g.bev1);
     (void)hipEventCreate(&g.t0);
@@ -281,7 +282,13 @@ extern "C" ds3_hip_buffer_t *ds3_hip_buffer_alloc(size_t bytes)
     void *p = nullptr;
     const size_t padded = ((bytes + 255) & ~(size_t)255) + kAllocPad;
     if (hipMalloc(&p, padded) != hipSuccess) return nullptr;
-    (void)hipMemset(p, 0, padded);
+    // Zero on the library stream and wait: the stream is non-blocking, so a
+    // null-stream memset could still be running when a later kernel on the
+    // library stream writes the buffer, and then overwrite its output.
+    if (hipMemsetAsync(p, 0, padded, g.stream) != hipSuccess || hipStreamSynchronize(g.stream) != hipSuccess) {
+        (void)hipFree(p);
+        return nullptr;
+    }
     auto *b = (ds3_hip_buffer_t *)calloc(1, sizeof(ds3_hip_buffer_t));
     if (!b) {
         (void)hipFree(p);

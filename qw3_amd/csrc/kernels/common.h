@@ -307,20 +307,58 @@ __device__ __forceinline__ void fma4(uint32_t x02, uint32_t x13, uint32_t mask, 
 }
 
 // ---------------------------------------------------------------------------
-// Raw bytes of the two units (g, g+4) of one row in 256-wide K step s, held
-// in registers so the loads for step s+1 can be in flight while step s is
-// decoded.  decode(hv) yields unit g + 4*hv exactly as unit_decode does.
+// Raw bytes of the two units (g, g+4) of one row in one 256-wide K step, held
+// in registers while they are decoded.  load(base, sh, g) reads the step's
+// quantised block of the row from base + sh, where base is 16-byte aligned
+// (the row's staging area in LDS) and sh < 16 the block's byte offset in it;
+// alignment is worked out on sh, never on pointer bits.  decode(hv) yields
+// unit g + 4*hv exactly as unit_decode does.
 // ---------------------------------------------------------------------------
 template <int TYPE> struct RawUnits;
 
+// Reads from LDS by byte address through inline asm, with their own
+// s_waitcnt lgkmcnt(0) in the same statement.  The grouped kernels stream
+// weights into LDS with global_load_lds DMAs; the compiler treats any LDS
+// access it sees as possibly aliasing those and would wait for every DMA in
+// flight, so the hot loops keep their LDS traffic in asm and order it
+// themselves (vmcnt waits for the DMAs, lgkmcnt here, s_barrier).
+
 template <> struct RawUnits<T_Q4_K> {
     uint4 hdr, q0, q1;
-    __device__ __forceinline__ void load(const uint8_t *row, int s, int g)
+    __device__ __forceinline__ void load(const uint8_t *base, int sh, int g)
     {
-        const uint8_t *blk = row + (size_t)s * 144;
+        const uint8_t *blk = base + sh;              // sh == 0: Q4_K blocks are staged 16-byte aligned
         hdr = *(const uint4 *)blk;
         q0 = *(const uint4 *)(blk + 16 + 16 * g);
         q1 = *(const uint4 *)(blk + 16 + 16 * (g + 4));
+    }
+    // any alignment, straight from global memory (dword loads + funnel shifts)
+    __device__ __forceinline__ void load_global(const uint8_t *blk, int g)
+    {
+        const uint8_t *p[3] = { blk, blk + 16 + 16 * g, blk + 16 + 16 * (g + 4) };
+        uint32_t w[3][4];
+#pragma unroll
+        for (int f = 0; f < 3; f++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) w[f][i] = ld_u32_a2(p[f] + 4 * i);
+        hdr = make_uint4(w[0][0], w[0][1], w[0][2], w[0][3]);
+        q0 = make_uint4(w[1][0], w[1][1], w[1][2], w[1][3]);
+        q1 = make_uint4(w[2][0], w[2][1], w[2][2], w[2][3]);
+    }
+    // base: LDS byte address of the row's 16-byte aligned block
+    __device__ __forceinline__ void load_lds(uint32_t base, int g)
+    {
+        typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+        u4v h, a, b;
+        asm volatile("ds_read_b128 %0, %3\n\t"
+                     "ds_read_b128 %1, %4\n\t"
+                     "ds_read_b128 %2, %5\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(h), "=&v"(a), "=&v"(b)
+                     : "v"(base), "v"(base + 16 + 16 * g), "v"(base + 16 + 16 * (g + 4)));
+        hdr = make_uint4(h.x, h.y, h.z, h.w);
+        q0 = make_uint4(a.x, a.y, a.z, a.w);
+        q1 = make_uint4(b.x, b.y, b.z, b.w);
     }
     // fragments p = 0..3 of unit g + 4*hv: low nibbles of bytes 0-7, 8-15,
     // then high nibbles of bytes 0-7, 8-15 (unit_decode's segment order)
@@ -333,7 +371,8 @@ template <> struct RawUnits<T_Q4_K> {
         q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1), sc0, mn0);
         q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1) + 1, sc1, mn1);
         const float dl = d * sc0, dh = d * sc1;
-        const float cl = -(1024.0f * dl) - dmin * mn0, ch = -(1024.0f * dh) - dmin * mn1;
+        const float cl = -(1024.0f * dl) - dmin * mn0;
+        const float dh16 = dh * 0.0625f, ch16 = -(64.0f * dh) - dmin * mn1;
         const uint32_t qw[4] = { q.x, q.y, q.z, q.w };
         const uint32_t mg = vgpr_magic();
 #pragma unroll
@@ -342,8 +381,10 @@ template <> struct RawUnits<T_Q4_K> {
 #pragma unroll
             for (int dd = 0; dd < 2; dd++) {
                 const uint32_t x = qw[2 * (p & 1) + dd];
+                // high nibbles stay in place: fp16 1024 + 16*code, so the
+                // scale is dh/16 (exact) and the constant -(64*dh + mh)
                 if (p < 2) fma4(x, x >> 8, 0x000f000fu, mg, dl, cl, w + 4 * dd);
-                else fma4(x >> 4, x >> 12, 0x000f000fu, mg, dh, ch, w + 4 * dd);
+                else fma4(x, x >> 8, 0x00f000f0u, mg, dh16, ch16, w + 4 * dd);
             }
 #pragma unroll
             for (int i = 0; i < 8; i++) fr[p][i] = w[i];
@@ -377,22 +418,59 @@ template <> struct RawUnits<T_Q4_K> {
 template <> struct RawUnits<T_Q6_K> {
     uint32_t f[2][4][3];      // [hv][ql_lo, ql_hi, qh, scales][dwords]
     uint32_t dw, sh;
-    __device__ __forceinline__ void load(const uint8_t *row, int s, int g)
+    __device__ __forceinline__ void load(const uint8_t *base, int sh16, int g)
     {
-        const uint8_t *blk = row + (size_t)s * 210;
-        const uintptr_t a = (uintptr_t)blk;
-        sh = (uint32_t)(a & 3);
-        const uint8_t *base = (const uint8_t *)(a & ~(uintptr_t)3);
+        sh = (uint32_t)(sh16 & 3);
+        const uint8_t *b4 = base + (sh16 & ~3);     // dword-aligned start at or below the block
 #pragma unroll
         for (int hv = 0; hv < 2; hv++) {
             const int off[4] = { 64 * hv + 8 * g, 64 * hv + 32 + 8 * g, 128 + 32 * hv + 8 * g, 192 + 8 * hv };
 #pragma unroll
             for (int fi = 0; fi < 4; fi++) {
-                const uint32_t *q = (const uint32_t *)(base + off[fi]);
+                const uint32_t *q = (const uint32_t *)(b4 + off[fi]);
                 f[hv][fi][0] = q[0]; f[hv][fi][1] = q[1]; f[hv][fi][2] = q[2];
             }
         }
-        dw = ld_u16(blk + 208);
+        dw = ld_u16(base + sh16 + 208);
+    }
+    // base: LDS byte address of the 16-byte aligned chunk run holding the
+    // block at byte offset sh16
+    __device__ __forceinline__ void load_lds(uint32_t base, int sh16, int g)
+    {
+        sh = (uint32_t)(sh16 & 3);
+        const uint32_t b4 = base + (uint32_t)(sh16 & ~3), bg = b4 + 8 * g;
+        typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+        u2v r[12];
+        uint32_t d16;
+        // fields (dword offsets, three consecutive dwords each): from bg
+        // (= b4 + 8g) ql_lo 0 | 16, ql_hi 8 | 24, qh 32 | 40 for half 0 | 1;
+        // from b4 the scales 48 | 50
+        asm volatile("ds_read2_b32 %0, %13 offset1:1\n\t"
+                     "ds_read2_b32 %1, %13 offset0:2 offset1:8\n\t"
+                     "ds_read2_b32 %2, %13 offset0:9 offset1:10\n\t"
+                     "ds_read2_b32 %3, %13 offset0:32 offset1:33\n\t"
+                     "ds_read2_b32 %4, %13 offset0:34 offset1:16\n\t"
+                     "ds_read2_b32 %5, %13 offset0:17 offset1:18\n\t"
+                     "ds_read2_b32 %6, %13 offset0:24 offset1:25\n\t"
+                     "ds_read2_b32 %7, %13 offset0:26 offset1:40\n\t"
+                     "ds_read2_b32 %8, %13 offset0:41 offset1:42\n\t"
+                     "ds_read2_b32 %9, %14 offset0:48 offset1:49\n\t"
+                     "ds_read2_b32 %10, %14 offset0:50 offset1:51\n\t"
+                     "ds_read2_b32 %11, %14 offset0:52 offset1:52\n\t"
+                     "ds_read_u16 %12, %15\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]),
+                       "=&v"(r[7]), "=&v"(r[8]), "=&v"(r[9]), "=&v"(r[10]), "=&v"(r[11]), "=&v"(d16)
+                     : "v"(bg), "v"(b4), "v"(base + (uint32_t)sh16 + 208));
+        f[0][0][0] = r[0].x; f[0][0][1] = r[0].y; f[0][0][2] = r[1].x;
+        f[0][1][0] = r[1].y; f[0][1][1] = r[2].x; f[0][1][2] = r[2].y;
+        f[0][2][0] = r[3].x; f[0][2][1] = r[3].y; f[0][2][2] = r[4].x;
+        f[1][0][0] = r[4].y; f[1][0][1] = r[5].x; f[1][0][2] = r[5].y;
+        f[1][1][0] = r[6].x; f[1][1][1] = r[6].y; f[1][1][2] = r[7].x;
+        f[1][2][0] = r[7].y; f[1][2][1] = r[8].x; f[1][2][2] = r[8].y;
+        f[0][3][0] = r[9].x; f[0][3][1] = r[9].y; f[0][3][2] = r[10].x;
+        f[1][3][0] = r[10].x; f[1][3][1] = r[10].y; f[1][3][2] = r[11].x;
+        dw = d16;
     }
     // fragment t of unit (half hv, j = g): outputs 32t + 8g + i
     __device__ __forceinline__ void decode_frags(int hv, int g, half8_t (&fr)[4]) const
@@ -455,16 +533,52 @@ template <> struct RawUnits<T_Q6_K> {
 template <> struct RawUnits<T_Q8_0> {
     uint32_t q[2][9];
     uint32_t sh[2];
-    __device__ __forceinline__ void load(const uint8_t *row, int s, int g)
+    __device__ __forceinline__ void load(const uint8_t *base, int sh16, int g)
     {
 #pragma unroll
         for (int hv = 0; hv < 2; hv++) {
-            const uintptr_t a = (uintptr_t)(row + (size_t)(8 * s + g + 4 * hv) * 34);
-            sh[hv] = (uint32_t)(a & 3);
-            const uint32_t *p = (const uint32_t *)(a & ~(uintptr_t)3);
+            const int o = sh16 + (g + 4 * hv) * 34;  // the unit's 34-byte block
+            sh[hv] = (uint32_t)(o & 3);
+            const uint32_t *p = (const uint32_t *)(base + (o & ~3));
 #pragma unroll
             for (int i = 0; i < 9; i++) q[hv][i] = p[i];
         }
+    }
+    // base: LDS byte address of the 16-byte aligned chunk run holding the
+    // step's first block at byte offset sh16
+    __device__ __forceinline__ void load_lds(uint32_t base, int sh16, int g)
+    {
+        typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+        uint32_t a4[2];
+#pragma unroll
+        for (int hv = 0; hv < 2; hv++) {
+            const int o = sh16 + (g + 4 * hv) * 34;  // the unit's 34-byte block
+            sh[hv] = (uint32_t)(o & 3);
+            a4[hv] = base + (uint32_t)(o & ~3);
+        }
+        u2v r[8];
+        uint32_t t0, t1;
+        asm volatile("ds_read2_b32 %0, %10 offset1:1\n\t"
+                     "ds_read2_b32 %1, %10 offset0:2 offset1:3\n\t"
+                     "ds_read2_b32 %2, %10 offset0:4 offset1:5\n\t"
+                     "ds_read2_b32 %3, %10 offset0:6 offset1:7\n\t"
+                     "ds_read_b32 %8, %10 offset:32\n\t"
+                     "ds_read2_b32 %4, %11 offset1:1\n\t"
+                     "ds_read2_b32 %5, %11 offset0:2 offset1:3\n\t"
+                     "ds_read2_b32 %6, %11 offset0:4 offset1:5\n\t"
+                     "ds_read2_b32 %7, %11 offset0:6 offset1:7\n\t"
+                     "ds_read_b32 %9, %11 offset:32\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]),
+                       "=&v"(r[7]), "=&v"(t0), "=&v"(t1)
+                     : "v"(a4[0]), "v"(a4[1]));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            q[0][2 * i] = r[i].x; q[0][2 * i + 1] = r[i].y;
+            q[1][2 * i] = r[4 + i].x; q[1][2 * i + 1] = r[4 + i].y;
+        }
+        q[0][8] = t0;
+        q[1][8] = t1;
     }
     __device__ __forceinline__ void decode_frags(int hv, int g, half8_t (&fr)[4]) const
     {
