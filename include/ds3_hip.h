@@ -207,9 +207,8 @@ int ds3_hip_moe_ffn_batch(
     uint32_t n_tokens, uint32_t n_embd, uint32_t n_expert, uint32_t n_used, uint32_t n_ff_exp,
     uint64_t router_row_stride, ds3_hip_type_t router_type, bool norm_topk_prob);
 
-/* Router only, for T tokens: logits, then indices/scores [T][n_used] with the
- * near-tie margin guard (selection matches the reference's sequential-sum
- * logits except for exact ties). */
+/* Router only, for T tokens: logits (bit-identical to the reference's
+ * sequential fp32 sums), then indices/scores [T][n_used]. */
 int ds3_hip_moe_route(const ds3_hip_buffer_t *input, const ds3_hip_buffer_t *w_gate_inp,
                       ds3_hip_buffer_t *gate_logits, ds3_hip_buffer_t *indices, ds3_hip_buffer_t *scores,
                       uint32_t n_tokens, uint32_t n_embd, uint32_t n_expert, uint32_t n_used,
@@ -231,10 +230,6 @@ int ds3_hip_dequantize(const ds3_hip_buffer_t *src, uint64_t src_offset, ds3_hip
  * n_tokens >= min_tokens, the per-token GEMV path otherwise.  0 restores the
  * default.  Returns the previous value. */
 int ds3_hip_set_prefill_min_tokens(int min_tokens);
-
-/* Number of tokens whose routing took the exact-recompute margin guard since
- * init (diagnostic). */
-int64_t ds3_hip_guard_count(void);
 
 /* Per-kernel timing with HIP events on the library stream.  While enabled,
  * each kernel launch is bracketed by an event pair; ds3_hip_kernel_stats

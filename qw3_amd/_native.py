@@ -62,7 +62,6 @@ SIGNATURES: dict[str, tuple] = {
     "ds3_hip_moe_bucket": (C.c_int, [P, P, U32, U32, U32, P, P, P, P, P]),
     "ds3_hip_dequantize": (C.c_int, [P, U64, I32, U64, P]),
     "ds3_hip_set_prefill_min_tokens": (C.c_int, [C.c_int]),
-    "ds3_hip_guard_count": (I64, []),
     "ds3_hip_kernel_timing": (None, [C.c_int]),
     "ds3_hip_kernel_timing_reset": (None, []),
     "ds3_hip_kernel_timing_only": (None, [C.c_char_p]),

@@ -44,7 +44,6 @@ struct State {
     size_t ws_bytes = 0;
     int32_t *zero_idx = nullptr;     // device {0}
     float *one_f = nullptr;          // device {1.0f}
-    int32_t *guard = nullptr;        // device guard counter
     int prefill_min = kDefaultPrefillMin;
     // reference-style profiling (src/ds3_metal.m:2868-2885)
     bool profile = false;
@@ -238,13 +237,10 @@ extern "C" int ds3_hip_init(void)
     if (hipMalloc(&consts, 256) != hipSuccess) return -1;
     g.zero_idx = (int32_t *)consts;
     g.one_f = (float *)((uint8_t *)consts + 64);
-    g.guard = (int32_t *)((uint8_t *)consts + 128);
     const int32_t zi = 0;
     const float one = 1.0f;
     (void)hipMemcpy(g.zero_idx, &zi, sizeof zi, hipMemcpyHostToDevice);
     (void)hipMemcpy(g.one_f, &one, sizeof one, hipMemcpyHostToDevice);
-    (void)hipMemsetAsync(g.guard, 0, sizeof(int32_t), g.stream);
-    (void)hipStreamSynchronize(g.stream);
     (void)hipEventCreate(&g.bev0);
     (void)hipEventCreate(&g.bev1);
     (void)hipEventCreate(&g.t0);
@@ -592,30 +588,24 @@ bool moe_limits_ok(uint32_t n_expert, uint32_t n_used)
 namespace {
 
 struct RouteBufs {
-    float *logits;       // [T][E] logits actually used (output)
+    float *logits;       // [T][E] router logits (output)
     int32_t *idx;
     float *scores;
-    float *part;         // [nparts][T][E] split-K partial logits (MFMA router)
-    float *wmax;         // [nparts] per-chunk max row sum of squares (MFMA router)
-    float *xsq;          // [nparts][T] per-chunk sum of x^2 (MFMA router)
-    float *wn_rows;      // [E] row sums of squares (GEMV router)
-    _Float16 *x16;       // optional [T][n_embd] fp16 copy of x, written by the MFMA router
+    float *wf32;         // [E][n_embd] FP32 copy of router rows stored in another type
+    _Float16 *x16;       // optional [T][n_embd] fp16 copy of x, written by the router
 };
 
 // Scratch of route_tokens beyond the output buffers, laid out from `base`.
 struct RouteScratch {
-    size_t o_part, o_wmax, o_xsq, o_wn, bytes;
+    size_t o_wf32, bytes;
 };
 
 RouteScratch route_scratch(int T, uint32_t n_embd, uint32_t n_expert)
 {
-    const int np = router_parts(T, (int)n_embd);
+    (void)T;
     Bump b;
     RouteScratch r;
-    r.o_part = b.take((size_t)np * T * n_expert * 4);
-    r.o_wmax = b.take((size_t)np * 4);
-    r.o_xsq = b.take((size_t)np * T * 4);
-    r.o_wn = b.take((size_t)n_expert * 4);
+    r.o_wf32 = b.take((size_t)n_expert * n_embd * 4);
     r.bytes = b.off;
     return r;
 }
@@ -623,41 +613,24 @@ RouteScratch route_scratch(int T, uint32_t n_embd, uint32_t n_expert)
 RouteBufs route_bufs(uint8_t *base, const RouteScratch &r, float *logits, int32_t *idx, float *scores,
                      _Float16 *x16)
 {
-    return RouteBufs{ logits, idx, scores, (float *)(base + r.o_part), (float *)(base + r.o_wmax),
-                      (float *)(base + r.o_xsq), (float *)(base + r.o_wn), x16 };
+    return RouteBufs{ logits, idx, scores, (float *)(base + r.o_wf32), x16 };
 }
 
-// Router logits + softmax/top-k/renorm for T tokens.  Returns 1 in *x16_done
-// when the MFMA router also wrote rb.x16.
+// Router logits + softmax/top-k/renorm for T tokens.  Sets *x16_done when the
+// router also wrote rb.x16.
 int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstride, int rtype, int T, uint32_t n_embd,
                  uint32_t n_expert, uint32_t n_used, bool norm, const RouteBufs &rb, bool *x16_done = nullptr)
 {
     hipError_t e;
-    RouteArgs ra{};
-    if (x16_done) *x16_done = false;
-    if (router_mfma_ok(rtype, (int)n_embd, (int)n_expert, x, cptr(router), rstride)) {
-        const int np = router_parts(T, (int)n_embd);
-        {
-            KScope ks("router_logits");
-            e = launch_router_logits(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, np, rb.part,
-                                     rb.wmax, rb.xsq, rb.x16, g.stream);
-        }
-        ra.logits = rb.part;
-        ra.nparts = np;
-        ra.part_stride = (int64_t)T * n_expert;
-        ra.logits_out = rb.logits;
-        ra.wmax_parts = rb.wmax;
-        ra.xsq_parts = rb.xsq;
-        if (x16_done) *x16_done = rb.x16 != nullptr;
-    } else {
+    {
         KScope ks("router_logits");
-        e = launch_gemv(rtype, x, n_embd, cptr(router), rstride, rb.logits, n_expert, T, (int)n_expert, (int)n_embd,
-                        rb.wn_rows, g.stream);
-        ra.logits = rb.logits;
-        ra.logits_out = nullptr;
-        ra.wn_rows = rb.wn_rows;
+        e = launch_router_seq(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, rb.wf32, rb.logits,
+                              n_expert, rb.x16, g.stream);
     }
     if (e != hipSuccess) return report(e, "router logits");
+    if (x16_done) *x16_done = rb.x16 != nullptr;
+    RouteArgs ra{};
+    ra.logits = rb.logits;
     ra.idx = rb.idx;
     ra.scores = rb.scores;
     ra.T = T;
@@ -666,12 +639,6 @@ int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstrid
     ra.logit_stride = n_expert;
     ra.out_stride = n_used;
     ra.norm = norm;
-    ra.x = x;
-    ra.K = (int)n_embd;
-    ra.rtype = rtype;
-    ra.rw = cptr(router);
-    ra.rstride = rstride;
-    ra.guard_count = g.guard;
     KScope ks("router_topk");
     return report(launch_route(ra, g.stream), "router topk");
 }
@@ -719,9 +686,9 @@ extern "C" int ds3_hip_moe_ffn(
     }
     if (n_embd == 0 || n_expert == 0 || n_used == 0 || n_ff_exp == 0) return -1;
     if (n_used > n_expert) return -1;
-    if (!moe_limits_ok(n_expert, n_used) || !gemv_type_ok(router_type, (int)n_embd) || !ensure_init()) {
-        if (!gemv_type_ok(router_type, (int)n_embd))
-            fprintf(stderr, "ds3_hip: router type %d with n_embd=%u unsupported\n", router_type, n_embd);
+    if (!moe_limits_ok(n_expert, n_used) || !router_seq_type_ok(router_type, (int)n_embd) || !ensure_init()) {
+        if (!router_seq_type_ok(router_type, (int)n_embd))
+            fprintf(stderr, "ds3_hip: router type %d unsupported\n", router_type);
         return -1;
     }
     if (!fits(input, (size_t)n_embd * 4, "input") || !fits(output, (size_t)n_embd * 4, "output") ||
@@ -760,10 +727,21 @@ extern "C" int ds3_hip_moe_ffn_router(const ds3_hip_buffer_t *input, const ds3_h
                                       ds3_hip_buffer_t *gate_logits, uint32_t n_embd, uint32_t n_expert,
                                       uint64_t router_row_stride, ds3_hip_type_t router_type)
 {
-    if (router_type == T_F32)
-        return ds3_hip_vec_matmul_f32(input, w_gate_inp, gate_logits, n_embd, n_expert, router_row_stride);
-    return ds3_hip_vec_matmul_quantized(input, w_gate_inp, gate_logits, n_embd, n_expert, router_row_stride,
-                                        router_type);
+    // the logits of the reference's sequential fp32 sums, bit for bit
+    if (!input || !w_gate_inp || !gate_logits || n_embd == 0 || n_expert == 0 || n_expert > 256 ||
+        !router_seq_type_ok(router_type, (int)n_embd) || !ensure_init())
+        return -1;
+    if (!fits(input, (size_t)n_embd * 4, "input") || !fits(gate_logits, (size_t)n_expert * 4, "gate_logits") ||
+        !fits(w_gate_inp, (size_t)n_expert * router_row_stride, "router"))
+        return -1;
+    const RouteScratch rs = route_scratch(1, n_embd, n_expert);
+    uint8_t *ws = ws_get(rs.bytes);
+    if (!ws) return -1;
+    KScope ks("router_logits");
+    return finish(launch_router_seq(fptr(input), 1, (int)n_embd, (int)n_expert, router_type, cptr(w_gate_inp),
+                                    router_row_stride, (float *)(ws + rs.o_wf32), fptr(gate_logits), n_expert,
+                                    nullptr, g.stream),
+                  "moe_ffn_router");
 }
 
 // reference src/ds3_metal.m:2172-2290
@@ -881,7 +859,7 @@ extern "C" int ds3_hip_moe_route(const ds3_hip_buffer_t *input, const ds3_hip_bu
     if (!input || !w_gate_inp || !indices || !scores || n_tokens == 0 || n_embd == 0 || n_expert == 0 ||
         n_used == 0 || n_used > n_expert || !ensure_init())
         return -1;
-    if (!moe_limits_ok(n_expert, n_used) || !gemv_type_ok(router_type, (int)n_embd)) return -1;
+    if (!moe_limits_ok(n_expert, n_used) || !router_seq_type_ok(router_type, (int)n_embd)) return -1;
     const size_t T = n_tokens;
     if (!fits(input, T * n_embd * 4, "input") || !fits(indices, T * n_used * 4, "indices") ||
         !fits(scores, T * n_used * 4, "scores") || !fits(gate_logits, T * n_expert * 4, "gate_logits"))
@@ -941,8 +919,8 @@ extern "C" int ds3_hip_moe_ffn_batch(
         !quant_type_ok_for_moe(down_type, n_ff_exp, "down"))
         return -1;
     if (!moe_limits_ok(n_expert, n_used) || !ensure_init()) return -1;
-    if (!gemv_type_ok(router_type, (int)n_embd)) {
-        fprintf(stderr, "ds3_hip: router type %d with n_embd=%u unsupported\n", router_type, n_embd);
+    if (!router_seq_type_ok(router_type, (int)n_embd)) {
+        fprintf(stderr, "ds3_hip: router type %d unsupported\n", router_type);
         return -1;
     }
     const size_t T = n_tokens;
@@ -1070,15 +1048,6 @@ extern "C" int ds3_hip_set_prefill_min_tokens(int min_tokens)
     const int prev = g.prefill_min;
     g.prefill_min = min_tokens > 0 ? min_tokens : kDefaultPrefillMin;
     return prev;
-}
-
-extern "C" int64_t ds3_hip_guard_count(void)
-{
-    if (!g.inited) return 0;
-    int32_t v = 0;
-    (void)hipStreamSynchronize(g.stream);
-    (void)hipMemcpy(&v, g.guard, sizeof v, hipMemcpyDeviceToHost);
-    return v;
 }
 
 // ===========================================================================

@@ -29,46 +29,29 @@ hipError_t launch_gemv(int type, const float *A, int64_t lda, const uint8_t *w, 
 
 bool gemv_type_ok(int type, int K);
 
+// Router logits in the reference's order: logits[t][e] (row stride ldl) =
+// x[t][0]*W[e][0] + x[t][1]*W[e][1] + ... summed left to right with every
+// product and sum rounded to fp32, bit-identical to the reference's.  Router
+// rows of any supported type (F32 / F16 / Q8_0 / Q4_K / Q6_K) at rw, rstride
+// bytes apart; rows other than 4-byte aligned F32 are first expanded into
+// wf32 [E][K].  If x16 != nullptr also x16[t][k] = (fp16) x[t][k].  E <= 256;
+// K a whole number of blocks of rtype.
+bool router_seq_type_ok(int rtype, int K);
+hipError_t launch_router_seq(const float *x, int T, int K, int E, int rtype, const uint8_t *rw, uint64_t rstride,
+                             float *wf32, float *logits, int64_t ldl, _Float16 *x16, hipStream_t s);
+
 // Router tail: logits [T][E] -> softmax -> top-k -> renorm, selected by
-// (prob desc, index asc) like the reference.  If x != nullptr the margin
-// guard recomputes near-tie logits in the reference's sequential order from
-// x [T][K] and router rows (rtype, rw, rstride); it then needs a bound on the
-// router row norms: wn_rows [E] (sum_k W[e][k]^2 per row) or wmax_parts
-// [nparts] (per K chunk, max over rows of the chunk's sum of squares).
-// xsq_parts [nparts][T] (per-chunk sum of x^2) saves re-reading x.
-// logits_out (may alias logits) receives the logits actually used.
+// (prob desc, index asc) like the reference.
 struct RouteArgs {
-    const float *logits;       // [nparts][T][E] when nparts > 1 (part_stride floats apart)
-    float *logits_out;
+    const float *logits;
     int32_t *idx;
     float *scores;
     int T, E, k;
     int64_t logit_stride;      // floats between tokens' logit rows
     int64_t out_stride;        // int32/float entries between tokens' idx/scores rows
     bool norm;
-    const float *x;
-    int K;
-    int rtype;
-    const uint8_t *rw;
-    uint64_t rstride;
-    const float *wn_rows = nullptr;
-    const float *wmax_parts = nullptr;
-    const float *xsq_parts = nullptr;
-    int32_t *guard_count;      // optional: number of tokens that took the exact recompute
-    int nparts = 1;
-    int64_t part_stride = 0;
 };
 hipError_t launch_route(const RouteArgs &a, hipStream_t s);
-
-// Router logits on fp32 MFMA as nparts split-K partials: part[p][t][e];
-// wmax[p] = max_e sum of W[e][k]^2 over chunk p; xsq[p][t] = sum of x[t][k]^2
-// over chunk p; if x16 != nullptr also x16[t][k] = (fp16) x[t][k].  F32 /
-// F16 / Q8_0 routers, K % 64 == 0, E % 16 == 0, E <= 256, x rows 16-byte
-// aligned, router rows aligned for their element loads.
-bool router_mfma_ok(int rtype, int K, int E, const void *x, const void *rw, uint64_t rstride);
-int router_parts(int T, int K);
-hipError_t launch_router_logits(const float *x, int T, int K, int E, int rtype, const uint8_t *rw, uint64_t rstride,
-                                int nparts, float *part, float *wmax, float *xsq, _Float16 *x16, hipStream_t s);
 
 // Decode (small T) expert products.
 //   h[slot][F] = silu(x[t] . Wg_e) * (x[t] . Wu_e), slot = t*n_used + k, e = idx[slot]

@@ -179,10 +179,6 @@ def set_prefill_min_tokens(n: int) -> int:
     return hip().ds3_hip_set_prefill_min_tokens(n)
 
 
-def guard_count() -> int:
-    return hip().ds3_hip_guard_count()
-
-
 def device_info() -> dict:
     arch = C.create_string_buffer(64)
     ncu = C.c_int()

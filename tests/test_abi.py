@@ -47,7 +47,7 @@ def test_compat_header_maps_every_metal_name():
     for name in _native.header_functions():
         metal = name.replace("ds3_hip_", "ds3_metal_")
         if name in ("ds3_hip_moe_ffn_batch", "ds3_hip_moe_route", "ds3_hip_moe_bucket", "ds3_hip_dequantize",
-                    "ds3_hip_set_prefill_min_tokens", "ds3_hip_guard_count", "ds3_hip_kernel_timing",
+                    "ds3_hip_set_prefill_min_tokens", "ds3_hip_kernel_timing",
                     "ds3_hip_kernel_timing_reset", "ds3_hip_kernel_timing_only", "ds3_hip_kernel_stats",
                     "ds3_hip_timer_start",
                     "ds3_hip_timer_stop_ms", "ds3_hip_device_info"):

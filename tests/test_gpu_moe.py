@@ -41,22 +41,34 @@ def q80():
     return Case(W.config_spec(5), seed=2026)
 
 
-def oracle_route(wr: np.ndarray, x: np.ndarray, k: int = W.N_USED):
+def oracle_route(wr: np.ndarray, x: np.ndarray, k: int = W.N_USED, with_logits: bool = False):
     idx = np.empty((x.shape[0], k), np.int32)
     sc = np.empty((x.shape[0], k), np.float32)
     probs = np.empty((x.shape[0], wr.shape[0]), np.float32)
+    logits = np.empty((x.shape[0], wr.shape[0]), np.float32)
     for t in range(x.shape[0]):
-        idx[t], sc[t], probs[t] = O.route(O.vec_matmul(x[t], wr), k, with_probs=True)
-    return idx, sc, probs
+        logits[t] = O.vec_matmul(x[t], wr)
+        idx[t], sc[t], probs[t] = O.route(logits[t], k, with_probs=True)
+    return (idx, sc, probs, logits) if with_logits else (idx, sc, probs)
+
+
+def route_raw(router: ds3.Buffer, rtype: int, x: np.ndarray, E: int, k: int):
+    """ds3_hip_moe_route on one router: (indices, scores, logits)."""
+    T, K = x.shape
+    xb = ds3.Buffer.from_array(x)
+    ib, sb, lb = ds3.Buffer.alloc(T * k * 4), ds3.Buffer.alloc(T * k * 4), ds3.Buffer.alloc(T * E * 4)
+    ds3.moe_route(xb, router, rtype, T, K, E, k, ib, sb, lb)
+    return ib.read(np.int32, (T, k)), sb.read(np.float32, (T, k)), lb.read(np.float32, (T, E))
 
 
 def gpu_route(case: Case, x: np.ndarray, k: int = W.N_USED):
-    T = x.shape[0]
-    s = case.spec
-    xb = ds3.Buffer.from_array(x)
-    ib, sb = ds3.Buffer.alloc(T * k * 4), ds3.Buffer.alloc(T * k * 4)
-    ds3.moe_route(xb, case.dev.router, s.router_type, T, s.n_embd, s.n_expert, k, ib, sb)
-    return ib.read(np.int32, (T, k)), sb.read(np.float32, (T, k))
+    return route_raw(case.dev.router, case.spec.router_type, x, case.spec.n_expert, k)
+
+
+def logit_bits_differ(got: np.ndarray, want: np.ndarray) -> int:
+    """Entries whose fp32 bit patterns differ (NaNs compare equal to NaNs)."""
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    return int((~same).sum())
 
 
 # ---------------------------------------------------------------------------
@@ -68,48 +80,52 @@ def test_route_indices_bit_exact(hip_ready, request, cfg, T):
     case = request.getfixturevalue(cfg)
     x = W.make_inputs({"real": 1, "uniform": 2, "zipf": 3, "q80": 5}[cfg], T, seed=77)
     print(f"  route {cfg} T={T}", flush=True)
-    gi, gs = gpu_route(case, x)
-    oi, osc, probs = oracle_route(case.wr, x)
+    gi, gs, gl = gpu_route(case, x)
+    oi, osc, probs, ol = oracle_route(case.wr, x, with_logits=True)
+    assert logit_bits_differ(gl, ol) == 0       # the reference's sequential fp32 sums, bit for bit
     assert index_mismatches(gi, oi, probs) == 0
-    same = gi == oi
-    rel = np.abs(gs[same] - osc[same]) / np.abs(osc[same])
-    print(f"    weights: max rel diff {rel.max():.2e}, guard total {ds3.guard_count()}", flush=True)
-    # logits differ from the sequential sum by ~1e-6, so weights by ~1e-6 relative
-    assert rel.max() < 2e-5
+    assert (gi == oi).all()
+    rel = np.abs(gs - osc) / np.abs(osc)
+    print(f"    weights: max rel diff {rel.max():.2e}", flush=True)
+    # same logits: the weights differ only by the device expf / division roundings
+    assert rel.max() < 2e-6
 
 
-def test_route_guard_resolves_near_ties(hip_ready):
+def test_route_near_ties(hip_ready):
     """Router rows 3 and 5 are row 0 shifted by ~1e-8 per element, so their
     logits sit ~5e-7 from row 0's: wider than a probability ulp, inside the
-    rounding noise of a reordered fp32 sum.  The margin guard must recompute
-    them in the reference's order and pick what the reference picks."""
+    rounding noise of a reordered fp32 sum.  Only the reference's own
+    summation order picks what the reference picks."""
     rng = np.random.default_rng(5)
     wr = (rng.standard_normal((16, 2048)) * 0.02).astype(np.float32)
     x = rng.standard_normal((64, 2048)).astype(np.float32)
     wr[3] = wr[0] + np.float32(1e-8)
     wr[5] = wr[0] - np.float32(1.5e-8)
-    router = ds3.Buffer.from_array(wr)
-    before = ds3.guard_count()
-    xb = ds3.Buffer.from_array(x)
-    ib, sb = ds3.Buffer.alloc(64 * 4 * 4), ds3.Buffer.alloc(64 * 4 * 4)
-    ds3.moe_route(xb, router, ds3.TYPE_F32, 64, 2048, 16, 4, ib, sb)
-    gi = ib.read(np.int32, (64, 4))
-    oi, _, probs = oracle_route(wr, x, 4)
-    fired = ds3.guard_count() - before
-    print(f"    guard fired for {fired} of 64 tokens", flush=True)
-    assert fired > 0
+    gi, _, gl = route_raw(ds3.Buffer.from_array(wr), ds3.TYPE_F32, x, 16, 4)
+    oi, _, probs, ol = oracle_route(wr, x, 4, with_logits=True)
+    assert logit_bits_differ(gl, ol) == 0
     assert index_mismatches(gi, oi, probs) == 0
+    assert (gi == oi).all()
 
 
 def _near_tie_router(type_: int, E: int, K: int, rng):
     """Router bytes whose rows 3 and 5 copy row 0 except one weight, moved by
-    one code (F32: by 1e-8 per element).  Returns (raw bytes, FP32 rows as the
+    one code or one fp16 ulp (F32: by 1e-8 per element).  Returns (raw bytes, FP32 rows as the
     oracle dequantises them, index of the changed weight)."""
     if type_ == ds3.TYPE_F32:
         wr = (rng.standard_normal((E, K)) * 0.02).astype(np.float32)
         wr[3] = wr[0] + np.float32(1e-8)
         wr[5] = wr[0] - np.float32(1.5e-8)
         return wr.reshape(-1).view(np.uint8).copy(), wr, None
+    if type_ == ds3.TYPE_F16:
+        h = (rng.standard_normal((E, K)) * 0.02).astype(np.float16)
+        h[3] = h[0]
+        h[5] = h[0]
+        j = 2048 + 5 if K > 2048 + 5 else 5
+        bits = h.view(np.uint16)
+        bits[3, j] += 1                       # one fp16 ulp either way
+        bits[5, j] -= 1
+        return h.reshape(-1).view(np.uint8).copy(), h.astype(np.float32), j
     raw = W.quant_matrix(type_, W.NORMAL, 4321, 7, E, K, 0.0, 0.02).reshape(E, -1).copy()
     raw[3] = raw[0]
     raw[5] = raw[0]
@@ -134,30 +150,63 @@ def _near_tie_router(type_: int, E: int, K: int, rng):
     return raw, wr, j
 
 
-@pytest.mark.parametrize("type_,E", [(ds3.TYPE_F32, 24), (ds3.TYPE_Q8_0, 16), (ds3.TYPE_Q8_0, 24),
-                                     (ds3.TYPE_Q4_K, 16), (ds3.TYPE_Q6_K, 16)])
-def test_route_guard_router_types(hip_ready, type_, E):
-    """Near ties on every router type and on both router paths (fp32 MFMA
-    logits for E % 16 == 0 with F32/F16/Q8_0 rows, the GEMV kernel
-    otherwise): the guard's exact recompute decodes each weight as the
-    reference's FP32 copy holds it, so selection matches the oracle."""
+@pytest.mark.parametrize("type_,E", [(ds3.TYPE_F32, 24), (ds3.TYPE_F16, 16), (ds3.TYPE_Q8_0, 16),
+                                     (ds3.TYPE_Q8_0, 24), (ds3.TYPE_Q4_K, 16), (ds3.TYPE_Q6_K, 16)])
+def test_route_router_types(hip_ready, type_, E):
+    """Near ties on every router type, E not a multiple of the 64 experts of
+    a wave included: the router rows are expanded to the values of the
+    reference's FP32 copy and summed in its order, so logits are bit-exact
+    and selection matches the oracle."""
     K, T, k = 2048, 64, 4
     rng = np.random.default_rng(9)
     raw, wr, j = _near_tie_router(type_, E, K, rng)
     x = rng.standard_normal((T, K)).astype(np.float32)
     if j is not None:
         x[:, j] = np.float32(1e-3)            # one code step of that weight moves the logit ~1e-7
-    router = ds3.Buffer.from_array(raw)
-    before = ds3.guard_count()
-    xb = ds3.Buffer.from_array(x)
-    ib, sb = ds3.Buffer.alloc(T * k * 4), ds3.Buffer.alloc(T * k * 4)
-    ds3.moe_route(xb, router, type_, T, K, E, k, ib, sb)
-    gi = ib.read(np.int32, (T, k))
-    oi, _, probs = oracle_route(wr, x, k)
-    fired = ds3.guard_count() - before
-    print(f"    {ds3.TYPE_NAMES[type_]} E={E}: guard fired for {fired} of {T} tokens", flush=True)
-    assert fired > 0
+    gi, _, gl = route_raw(ds3.Buffer.from_array(raw), type_, x, E, k)
+    oi, _, probs, ol = oracle_route(wr, x, k, with_logits=True)
+    print(f"    {ds3.TYPE_NAMES[type_]} E={E}", flush=True)
+    assert logit_bits_differ(gl, ol) == 0
     assert index_mismatches(gi, oi, probs) == 0
+    assert (gi == oi).all()
+
+
+@pytest.mark.parametrize("type_", [ds3.TYPE_F32, ds3.TYPE_Q8_0, ds3.TYPE_Q4_K])
+def test_moe_ffn_router_logits(hip_ready, type_):
+    """ds3_hip_moe_ffn_router (one token): the reference's logits bit for bit."""
+    from qw3_amd._native import hip
+    K, E = 2048, 128
+    rng = np.random.default_rng(21)
+    raw, wr, _ = _near_tie_router(type_, E, K, rng)
+    x = rng.standard_normal(K).astype(np.float32)
+    lb = ds3.Buffer.alloc(E * 4)
+    assert hip().ds3_hip_moe_ffn_router(ds3.Buffer.from_array(x), ds3.Buffer.from_array(raw), lb, K, E,
+                                        ds3.row_bytes(type_, K), type_) == 0
+    assert logit_bits_differ(lb.read(np.float32, (E,)), O.vec_matmul(x, wr)) == 0
+
+
+@pytest.mark.parametrize("T,K,E,align", [(1, 2048, 128, 0), (5, 2048, 128, 0), (37, 1000, 72, 0),
+                                         (130, 2048, 128, 4), (1100, 512, 128, 0)])
+def test_route_logits_shapes(hip_ready, T, K, E, align):
+    """Ragged T (workgroup tails), K not a multiple of the 256-wide chunk or
+    of 4 (scalar loads), E not a multiple of 64, an x row start that is only
+    4-byte aligned, and T >= 1024 (8 tokens per workgroup)."""
+    rng = np.random.default_rng(T + K + E)
+    wr = (rng.standard_normal((E, K)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    k = 8
+    if align:
+        # the same rows behind a 4-byte shift: the router reads them through a view
+        base = ds3.Buffer.from_array(np.concatenate([np.zeros(1, np.float32), x.reshape(-1)]))
+        xb = base.view(align, T * K * 4)
+    else:
+        xb = ds3.Buffer.from_array(x)
+    ib, sb, lb = ds3.Buffer.alloc(T * k * 4), ds3.Buffer.alloc(T * k * 4), ds3.Buffer.alloc(T * E * 4)
+    ds3.moe_route(xb, ds3.Buffer.from_array(wr), ds3.TYPE_F32, T, K, E, k, ib, sb, lb)
+    gl = lb.read(np.float32, (T, E))
+    oi, _, probs, ol = oracle_route(wr, x, k, with_logits=True)
+    assert logit_bits_differ(gl, ol) == 0
+    assert (ib.read(np.int32, (T, k)) == oi).all()
 
 
 def test_topk_batch_entry_points(hip_ready):
