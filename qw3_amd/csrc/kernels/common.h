@@ -364,15 +364,28 @@ template <> struct RawUnits<T_Q4_K> {
     // then high nibbles of bytes 0-7, 8-15 (unit_decode's segment order)
     __device__ __forceinline__ void decode_frags(int hv, int g, half8_t (&fr)[4]) const
     {
-        const int c = g + 4 * hv;
         const uint4 q = hv ? q1 : q0;
+        // (scale, min) of sub-blocks j, j+1 of unit g + 4hv, j = 2*(g>>1) + 4hv,
+        // as two bytes each: get_scale_min_k4 (src/ds3_reference.c:76-85) on
+        // the pair at once.  hv 0: low 6 bits of bytes j, j+4; hv 1: low
+        // nibbles / high nibbles of bytes j+4 with the top 2 bits of bytes
+        // j-4 / j.
+        const uint32_t sh = (uint32_t)(g >> 1) * 16u;
+        const uint32_t a = hdr.y >> sh, b = hdr.z >> sh;
+        uint32_t scp, mp;
+        if (hv == 0) {
+            scp = a & 0x3f3fu;
+            mp = b & 0x3f3fu;
+        } else {
+            const uint32_t cw = hdr.w >> sh;
+            scp = (cw & 0x0f0fu) | ((a >> 2) & 0x3030u);
+            mp = ((cw >> 4) & 0x0f0fu) | ((b >> 2) & 0x3030u);
+        }
         const float d = h2f(hdr.x & 0xffffu), dmin = h2f(hdr.x >> 16);
-        float sc0, mn0, sc1, mn1;
-        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1), sc0, mn0);
-        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1) + 1, sc1, mn1);
-        const float dl = d * sc0, dh = d * sc1;
-        const float cl = -(1024.0f * dl) - dmin * mn0;
-        const float dh16 = dh * 0.0625f, ch16 = -(64.0f * dh) - dmin * mn1;
+        const float dl = d * (float)(scp & 0xffu);
+        const float dh16 = (d * 0.0625f) * (float)((scp >> 8) & 0xffu);   // exact: a power-of-two scale
+        const float cl = -(1024.0f * dl) - dmin * (float)(mp & 0xffu);
+        const float ch16 = -(1024.0f * dh16) - dmin * (float)((mp >> 8) & 0xffu);
         const uint32_t qw[4] = { q.x, q.y, q.z, q.w };
         const uint32_t mg = vgpr_magic();
 #pragma unroll

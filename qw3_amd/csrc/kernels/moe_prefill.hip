@@ -222,6 +222,8 @@ __device__ __forceinline__ void gm_issue(const GmRun<NB> &r, int v)
 // barrier (every wave's share of the activation tile has landed, and every
 // wave is done with buffer (u+1) & 1), issue the loads of step u+1, compute
 // step u.  vmcnt(0) holds whatever order the memory system returns in.
+// (A third weight stage for tiles of at most 32 tokens, and stores deferred
+// by one step, measured no faster on MI355X at T = 512.)
 template <int TYPE, int NB, int MB, bool INPLACE, class Epi>
 __device__ __forceinline__ void gm_run(const GmRun<NB> &r, const Epi &epi)
 {
@@ -256,7 +258,9 @@ __device__ __forceinline__ void gm_run(const GmRun<NB> &r, const Epi &epi)
         }
         gm_step<TYPE, NB, MB>(r.lds + (uint32_t)(buf * GM_ATILE), cur, r.lane, acc);
         if (cs == r.S - 1) {
-            epi.template store<MB>(acc, r.nt0 + ct);
+            typename Epi::template Out<MB> o;
+            epi.template finish<MB>(acc, r.nt0 + ct, o);
+            epi.template store<MB>(o);
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -338,20 +342,36 @@ __device__ __forceinline__ void gm_dma_map(GmRun<NB> &r, int lane, uint64_t stri
     }
 }
 
+// Epilogues: finish() turns a tile's accumulators into output values held
+// in registers (Out), store() writes them.  Lane (g = lane/16, m = lane%16)
+// of wave w holds rows 16mb + 4g + j of output column nt*tile_n + 16w + m.
 struct EpiGateUp {
     _Float16 *h16;
     int F, row0, mrows, tile_n;       // row0 = compacted position of the tile's first token
+    template <int MB> struct Out {
+        _Float16 v[MB][4];
+        int nt;
+    };
     template <int MB>
-    __device__ __forceinline__ void store(const floatx4 (&acc)[4][2], int nt) const
+    __device__ __forceinline__ void finish(const floatx4 (&acc)[4][2], int nt, Out<MB> &o) const
+    {
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) o.v[mb][j] = (_Float16)swiglu(acc[mb][0][j], acc[mb][1][j]);
+        o.nt = nt;
+    }
+    template <int MB>
+    __device__ __forceinline__ void store(const Out<MB> &o) const
     {
         const int lane = threadIdx.x & 63;
-        const int nrow = nt * tile_n + 16 * (threadIdx.x >> 6) + (lane & 15);
+        const int nrow = o.nt * tile_n + 16 * (threadIdx.x >> 6) + (lane & 15);
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int mr = 16 * mb + 4 * (lane >> 4) + j;
-                if (mr < mrows) h16[(int64_t)(row0 + mr) * F + nrow] = (_Float16)swiglu(acc[mb][0][j], acc[mb][1][j]);
+                if (mr < mrows) h16[(int64_t)(row0 + mr) * F + nrow] = o.v[mb][j];
             }
         }
     }
@@ -360,17 +380,30 @@ struct EpiGateUp {
 struct EpiDown {
     float *y;
     int N, row0, mrows, tile_n;
+    template <int MB> struct Out {
+        float v[MB][4];
+        int nt;
+    };
     template <int MB>
-    __device__ __forceinline__ void store(const floatx4 (&acc)[4][1], int nt) const
+    __device__ __forceinline__ void finish(const floatx4 (&acc)[4][1], int nt, Out<MB> &o) const
+    {
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) o.v[mb][j] = acc[mb][0][j];
+        o.nt = nt;
+    }
+    template <int MB>
+    __device__ __forceinline__ void store(const Out<MB> &o) const
     {
         const int lane = threadIdx.x & 63;
-        const int nrow = nt * tile_n + 16 * (threadIdx.x >> 6) + (lane & 15);
+        const int nrow = o.nt * tile_n + 16 * (threadIdx.x >> 6) + (lane & 15);
 #pragma unroll
         for (int mb = 0; mb < MB; mb++) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int mr = 16 * mb + 4 * (lane >> 4) + j;
-                if (mr < mrows) y[(int64_t)(row0 + mr) * N + nrow] = acc[mb][0][j];
+                if (mr < mrows) y[(int64_t)(row0 + mr) * N + nrow] = o.v[mb][j];
             }
         }
     }
