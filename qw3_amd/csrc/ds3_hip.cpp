@@ -43,6 +43,7 @@ struct State {
     uint8_t *ws = nullptr;
     size_t ws_bytes = 0;
     int32_t *zero_idx = nullptr;     // device {0}
+    int32_t *tickets = nullptr;      // 32 router tickets (zero between launches)
     float *one_f = nullptr;          // device {1.0f}
     int prefill_min = kDefaultPrefillMin;
     // reference-style profiling (src/ds3_metal.m:2868-2885)
@@ -237,6 +238,9 @@ extern "C" int ds3_hip_init(void)
     if (hipMalloc(&consts, 256) != hipSuccess) return -1;
     g.zero_idx = (int32_t *)consts;
     g.one_f = (float *)((uint8_t *)consts + 64);
+    g.tickets = (int32_t *)((uint8_t *)consts + 128);   // router token-group tickets, kept at zero between launches
+    if (hipMemsetAsync(g.tickets, 0, 128, g.stream) != hipSuccess || hipStreamSynchronize(g.stream) != hipSuccess)
+        return -1;
     const int32_t zi = 0;
     const float one = 1.0f;
     (void)hipMemcpy(g.zero_idx, &zi, sizeof zi, hipMemcpyHostToDevice);
@@ -621,14 +625,6 @@ RouteBufs route_bufs(uint8_t *base, const RouteScratch &r, float *logits, int32_
 int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstride, int rtype, int T, uint32_t n_embd,
                  uint32_t n_expert, uint32_t n_used, bool norm, const RouteBufs &rb, bool *x16_done = nullptr)
 {
-    hipError_t e;
-    {
-        KScope ks("router_logits");
-        e = launch_router_seq(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, rb.wf32, rb.logits,
-                              n_expert, rb.x16, g.stream);
-    }
-    if (e != hipSuccess) return report(e, "router logits");
-    if (x16_done) *x16_done = rb.x16 != nullptr;
     RouteArgs ra{};
     ra.logits = rb.logits;
     ra.idx = rb.idx;
@@ -639,6 +635,16 @@ int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstrid
     ra.logit_stride = n_expert;
     ra.out_stride = n_used;
     ra.norm = norm;
+    hipError_t e;
+    bool topk_done = false;
+    {
+        KScope ks("router_logits");
+        e = launch_router_seq(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, rb.wf32, rb.logits,
+                              n_expert, rb.x16, &ra, g.tickets, &topk_done, g.stream);
+    }
+    if (e != hipSuccess) return report(e, "router logits");
+    if (x16_done) *x16_done = rb.x16 != nullptr;
+    if (topk_done) return 0;                    // the router kernel also selected the experts
     KScope ks("router_topk");
     return report(launch_route(ra, g.stream), "router topk");
 }
@@ -740,7 +746,7 @@ extern "C" int ds3_hip_moe_ffn_router(const ds3_hip_buffer_t *input, const ds3_h
     KScope ks("router_logits");
     return finish(launch_router_seq(fptr(input), 1, (int)n_embd, (int)n_expert, router_type, cptr(w_gate_inp),
                                     router_row_stride, (float *)(ws + rs.o_wf32), fptr(gate_logits), n_expert,
-                                    nullptr, g.stream),
+                                    nullptr, nullptr, nullptr, nullptr, g.stream),
                   "moe_ffn_router");
 }
 

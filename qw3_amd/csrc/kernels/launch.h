@@ -34,12 +34,6 @@ bool gemv_type_ok(int type, int K);
 // product and sum rounded to fp32, bit-identical to the reference's.  Router
 // rows of any supported type (F32 / F16 / Q8_0 / Q4_K / Q6_K) at rw, rstride
 // bytes apart; rows other than 4-byte aligned F32 are first expanded into
-// wf32 [E][K].  If x16 != nullptr also x16[t][k] = (fp16) x[t][k].  E <= 256;
-// K a whole number of blocks of rtype.
-bool router_seq_type_ok(int rtype, int K);
-hipError_t launch_router_seq(const float *x, int T, int K, int E, int rtype, const uint8_t *rw, uint64_t rstride,
-                             float *wf32, float *logits, int64_t ldl, _Float16 *x16, hipStream_t s);
-
 // Router tail: logits [T][E] -> softmax -> top-k -> renorm, selected by
 // (prob desc, index asc) like the reference.
 struct RouteArgs {
@@ -52,6 +46,15 @@ struct RouteArgs {
     bool norm;
 };
 hipError_t launch_route(const RouteArgs &a, hipStream_t s);
+
+// wf32 [E][K].  If x16 != nullptr also x16[t][k] = (fp16) x[t][k].  E <= 256;
+// K a whole number of blocks of rtype.  With topk (describing these logits)
+// and tickets (zeroed device ints, left zeroed) the kernel may also run the
+// router tail for small T; *topk_done says whether it did.
+bool router_seq_type_ok(int rtype, int K);
+hipError_t launch_router_seq(const float *x, int T, int K, int E, int rtype, const uint8_t *rw, uint64_t rstride,
+                             float *wf32, float *logits, int64_t ldl, _Float16 *x16, const RouteArgs *topk,
+                             int *tickets, bool *topk_done, hipStream_t s);
 
 // Decode (small T) expert products.
 //   h[slot][F] = silu(x[t] . Wg_e) * (x[t] . Wu_e), slot = t*n_used + k, e = idx[slot]

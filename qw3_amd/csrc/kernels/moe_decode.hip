@@ -22,41 +22,56 @@ constexpr int DEC_TPB = 256;
 
 // PAIR: h = swiglu(gate, up).  !PAIR: h = gate projection only, with expert
 // offsets from table column `which` (unfused fallback for mixed types).
-template <int GT, int G, bool PAIR>
+// Lane group (G lanes) per row, UPL = K/32/G units per lane, RPW rows per
+// group: the trip counts are compile-time and rows past F are clamped (their
+// results dropped), so every load of a wave is issued before its first dot
+// product and the wave pays one memory round trip.
+template <int GT, int G, int UPL, bool PAIR>
 __global__ void __launch_bounds__(DEC_TPB)
 k_decode_gate_up(const float *__restrict__ x, int64_t ldx, const int32_t *__restrict__ idx, int n_used,
-                 ExpertWeights ew, int K, int F, int rows_per_wg, int which, float *__restrict__ h)
+                 ExpertWeights ew, int K, int F, int which, float *__restrict__ h)
 {
+    constexpr int GPW = WAVE / G, RPW = 2;
     const int slot = blockIdx.y;
     const int t = slot / n_used;
     const int e = idx[slot];
     const uint8_t *wg = expert_base(ew.gate, ew.table, e, PAIR ? 0 : which, (uint64_t)F, ew.gate_stride);
     const uint8_t *wu = PAIR ? expert_base(ew.up, ew.table, e, 1, (uint64_t)F, ew.up_stride) : wg;
     const float *xt = x + (int64_t)t * ldx;
-
-    constexpr int GPW = WAVE / G;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     const int gl = lane % G, grp = lane / G;
-    const int U = K / 32;
-    for (int rr = wave * GPW + grp; rr < rows_per_wg; rr += (DEC_TPB / WAVE) * GPW) {
-        const int r = blockIdx.x * rows_per_wg + rr;
-        const bool valid = r < F;
-        float ag = 0.f, au = 0.f;
-        if (valid) {
-            const uint8_t *grow = wg + (size_t)r * ew.gate_stride;
-            const uint8_t *urow = wu + (size_t)r * ew.up_stride;
-            for (int u = gl; u < U; u += G) {
-                ag += unit_dot<GT>(grow, u, xt);
-                if (PAIR) au += unit_dot<GT>(urow, u, xt);
-            }
+    const int r0 = (blockIdx.x * (DEC_TPB / WAVE) + wave) * GPW * RPW + grp;
+    float ag[RPW], au[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+        const int r = min(r0 + GPW * i, F - 1);
+        const uint8_t *grow = wg + (size_t)r * ew.gate_stride;
+        const uint8_t *urow = wu + (size_t)r * ew.up_stride;
+        ag[i] = 0.f;
+        au[i] = 0.f;
+        const int upl = UPL > 0 ? UPL : K / 32 / G;
+#pragma unroll
+        for (int j = 0; j < (UPL > 0 ? UPL : 1); j++) {
+            ag[i] += unit_dot<GT>(grow, gl + G * j, xt);
+            if (PAIR) au[i] += unit_dot<GT>(urow, gl + G * j, xt);
         }
-        ag = group_sum<G>(ag);
-        if (PAIR) au = group_sum<G>(au);
-        if (valid && gl == 0) h[(int64_t)slot * F + r] = PAIR ? swiglu(ag, au) : ag;
+        for (int j = (UPL > 0 ? UPL : 1); j < upl; j++) {   // shapes without a compile-time count
+            ag[i] += unit_dot<GT>(grow, gl + G * j, xt);
+            if (PAIR) au[i] += unit_dot<GT>(urow, gl + G * j, xt);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+        const int r = r0 + GPW * i;
+        const float a = group_sum<G>(ag[i]);
+        const float b = PAIR ? group_sum<G>(au[i]) : 0.f;
+        if (r < F && gl == 0) h[(int64_t)slot * F + r] = PAIR ? swiglu(a, b) : a;
     }
 }
 
-template <int DT, int G>
+// One wave per selected expert k, lane group (G lanes) per output row, UPL
+// units per lane with compile-time trip counts (all loads issued first).
+template <int DT, int G, int UPL>
 __global__ void __launch_bounds__(1024)
 k_decode_down(const float *__restrict__ h, const int32_t *__restrict__ idx, const float *__restrict__ wts,
               int n_used, ExpertWeights ew, int N, int F, int rows_per_wg, float *__restrict__ out,
@@ -70,35 +85,32 @@ k_decode_down(const float *__restrict__ h, const int32_t *__restrict__ idx, cons
     const uint8_t *wd = expert_base(ew.down, ew.table, e, 2, (uint64_t)N, ew.down_stride);
     const float *hs = h + (int64_t)slot * F;
 
-    constexpr int GPW = WAVE / G;
     const int lane = threadIdx.x & (WAVE - 1);
-    const int gl = lane % G, grp = lane / G;
-    const int U = F / 32;
-    for (int rr = grp; rr < rows_per_wg; rr += GPW) {
-        const int j = blockIdx.x * rows_per_wg + rr;
-        float acc = 0.f;
-        if (j < N) {
-            const uint8_t *row = wd + (size_t)j * ew.down_stride;
-            for (int u = gl; u < U; u += G) acc += unit_dot<DT>(row, u, hs);
-        }
-        acc = group_sum<G>(acc);
-        if (gl == 0) part[k * rows_per_wg + rr] = acc;
-    }
+    const int gl = lane % G, grp = lane / G;  // rows_per_wg == WAVE / G: one row per group
+    const int j = min(blockIdx.x * rows_per_wg + grp, N - 1);
+    const uint8_t *row = wd + (size_t)j * ew.down_stride;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < (UPL > 0 ? UPL : 1); i++) acc += unit_dot<DT>(row, gl + G * i, hs);
+    for (int i = (UPL > 0 ? UPL : 1); i < F / 32 / G; i++) acc += unit_dot<DT>(row, gl + G * i, hs);
+    acc = group_sum<G>(acc);
+    if (gl == 0) part[k * rows_per_wg + grp] = acc;
     __syncthreads();
     for (int rr = threadIdx.x; rr < rows_per_wg; rr += blockDim.x) {
-        const int j = blockIdx.x * rows_per_wg + rr;
-        if (j >= N) continue;
-        float *o = out + (int64_t)t * ldo + j;
+        const int jj = blockIdx.x * rows_per_wg + rr;
+        if (jj >= N) continue;
+        float *o = out + (int64_t)t * ldo + jj;
         {
 #pragma clang fp contract(off)
-            float acc = accumulate ? *o : 0.0f;
-            for (int kk = 0; kk < n_used; kk++) acc = acc + wts[t * n_used + kk] * part[kk * rows_per_wg + rr];
-            if (residual) acc = acc + residual[(int64_t)t * ldo + j];
-            *o = acc;
+            float a = accumulate ? *o : 0.0f;
+            for (int kk = 0; kk < n_used; kk++) a = a + wts[t * n_used + kk] * part[kk * rows_per_wg + rr];
+            if (residual) a = a + residual[(int64_t)t * ldo + jj];
+            *o = a;
         }
     }
 }
 
+// Lanes per row: the largest power of two <= 64 dividing the row's units.
 static int lanes_per_row(int units)
 {
     int g = 1;
@@ -118,6 +130,15 @@ static int lanes_per_row(int units)
     default: return hipErrorInvalidValue;                                       \
     }
 
+// Units per lane as a compile-time count for the shapes of the configs
+// (1: K = 2048 at 64 lanes, 3: K = 768 at 8 lanes); 0 = runtime loop.
+#define DS3_U_SWITCH(U, CALL)                                                   \
+    switch (U) {                                                                \
+    case 1: { constexpr int UV = 1; CALL; } break;                              \
+    case 3: { constexpr int UV = 3; CALL; } break;                              \
+    default: { constexpr int UV = 0; CALL; } break;                             \
+    }
+
 #define DS3_T_SWITCH(TY, CALL)                                                  \
     switch (TY) {                                                               \
     case T_F32: { constexpr int TV = T_F32; CALL; } break;                      \
@@ -127,25 +148,21 @@ static int lanes_per_row(int units)
     default: return hipErrorInvalidValue;                                       \
     }
 
+
 static hipError_t decode_gate_up_impl(const float *x, int64_t ldx, const int32_t *idx, int n_slots, int n_used,
                                       const ExpertWeights &ew, int K, int F, float *h, bool pair, int which,
                                       hipStream_t s)
 {
-    if (!gemv_type_ok(ew.gate_type, K) || n_slots <= 0) return hipErrorInvalidValue;
-    const int G = lanes_per_row(K / 32);
-    const int rows_step = (DEC_TPB / WAVE) * (WAVE / G);
-    // Two passes of the workgroup per block keeps ~768 WGs at T=1, F=768, G=64.
-    int rpw = rows_step * 2;
-    if (rpw > F) rpw = rows_step;
-    const dim3 grid((unsigned)((F + rpw - 1) / rpw), (unsigned)n_slots);
+    if (!gemv_type_ok(ew.gate_type, K) || n_slots <= 0 || F <= 0) return hipErrorInvalidValue;
+    const int G = lanes_per_row(K / 32), UPL = K / 32 / G;
+    const int rows_per_wg = (DEC_TPB / WAVE) * (WAVE / G) * 2;     // 2 rows per lane group
+    const dim3 grid((unsigned)((F + rows_per_wg - 1) / rows_per_wg), (unsigned)n_slots);
     if (pair) {
-        DS3_T_SWITCH(ew.gate_type, DS3_G_SWITCH(G, hipLaunchKernelGGL((k_decode_gate_up<TV, GV, true>), grid,
-                                                                      dim3(DEC_TPB), 0, s, x, ldx, idx, n_used, ew,
-                                                                      K, F, rpw, which, h)));
+        DS3_T_SWITCH(ew.gate_type, DS3_G_SWITCH(G, DS3_U_SWITCH(UPL, hipLaunchKernelGGL(
+            (k_decode_gate_up<TV, GV, UV, true>), grid, dim3(DEC_TPB), 0, s, x, ldx, idx, n_used, ew, K, F, which, h))));
     } else {
-        DS3_T_SWITCH(ew.gate_type, DS3_G_SWITCH(G, hipLaunchKernelGGL((k_decode_gate_up<TV, GV, false>), grid,
-                                                                      dim3(DEC_TPB), 0, s, x, ldx, idx, n_used, ew,
-                                                                      K, F, rpw, which, h)));
+        DS3_T_SWITCH(ew.gate_type, DS3_G_SWITCH(G, DS3_U_SWITCH(UPL, hipLaunchKernelGGL(
+            (k_decode_gate_up<TV, GV, UV, false>), grid, dim3(DEC_TPB), 0, s, x, ldx, idx, n_used, ew, K, F, which, h))));
     }
     return hipGetLastError();
 }
@@ -167,15 +184,15 @@ hipError_t launch_decode_down(const float *h, const int32_t *idx, const float *w
                               const ExpertWeights &ew, int N, int F, float *out, int64_t ldo,
                               const float *residual, bool accumulate, hipStream_t s)
 {
-    if (!gemv_type_ok(ew.down_type, F) || T <= 0 || n_used <= 0 || n_used > 16) return hipErrorInvalidValue;
-    const int G = lanes_per_row(F / 32);
-    const int gpw = WAVE / G;
-    const int rpw = gpw;                        // each wave covers its rows in one pass
+    if (!gemv_type_ok(ew.down_type, F) || T <= 0 || N <= 0 || n_used <= 0 || n_used > 16)
+        return hipErrorInvalidValue;
+    const int G = lanes_per_row(F / 32), UPL = F / 32 / G;
+    const int rpw = WAVE / G;                   // one row per lane group
     const dim3 grid((unsigned)((N + rpw - 1) / rpw), (unsigned)T);
     const size_t lds = (size_t)n_used * rpw * sizeof(float);
-    DS3_T_SWITCH(ew.down_type, DS3_G_SWITCH(G, hipLaunchKernelGGL((k_decode_down<TV, GV>), grid, dim3(n_used * WAVE), lds, s,
-                                                                  h, idx, wts, n_used, ew, N, F, rpw, out, ldo, residual,
-                                                                  accumulate ? 1 : 0)));
+    DS3_T_SWITCH(ew.down_type, DS3_G_SWITCH(G, DS3_U_SWITCH(UPL, hipLaunchKernelGGL(
+        (k_decode_down<TV, GV, UV>), grid, dim3(n_used * WAVE), lds, s, h, idx, wts, n_used, ew, N, F, rpw, out, ldo,
+        residual, accumulate ? 1 : 0))));
     return hipGetLastError();
 }
 

@@ -133,11 +133,47 @@ __device__ __forceinline__ void rs_sum(float &acc, const u32x4 (&w)[4], const u3
 // remain.  Loads complete in issue order, so the oldest chunk is then done.
 __device__ __forceinline__ void rs_vm_wait(int n)
 {
-    switch (n) {
-    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    switch (n) {           // n is wave-uniform; above 40 (never used) waits for all
+    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
     case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
+    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+    case 11: asm volatile("s_waitcnt vmcnt(11)" ::: "memory"); break;
+    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    case 13: asm volatile("s_waitcnt vmcnt(13)" ::: "memory"); break;
+    case 14: asm volatile("s_waitcnt vmcnt(14)" ::: "memory"); break;
+    case 15: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
     case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    case 17: asm volatile("s_waitcnt vmcnt(17)" ::: "memory"); break;
+    case 18: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+    case 19: asm volatile("s_waitcnt vmcnt(19)" ::: "memory"); break;
+    case 20: asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); break;
+    case 21: asm volatile("s_waitcnt vmcnt(21)" ::: "memory"); break;
+    case 22: asm volatile("s_waitcnt vmcnt(22)" ::: "memory"); break;
+    case 23: asm volatile("s_waitcnt vmcnt(23)" ::: "memory"); break;
+    case 24: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+    case 25: asm volatile("s_waitcnt vmcnt(25)" ::: "memory"); break;
+    case 26: asm volatile("s_waitcnt vmcnt(26)" ::: "memory"); break;
+    case 27: asm volatile("s_waitcnt vmcnt(27)" ::: "memory"); break;
+    case 28: asm volatile("s_waitcnt vmcnt(28)" ::: "memory"); break;
+    case 29: asm volatile("s_waitcnt vmcnt(29)" ::: "memory"); break;
+    case 30: asm volatile("s_waitcnt vmcnt(30)" ::: "memory"); break;
+    case 31: asm volatile("s_waitcnt vmcnt(31)" ::: "memory"); break;
     case 32: asm volatile("s_waitcnt vmcnt(32)" ::: "memory"); break;
+    case 33: asm volatile("s_waitcnt vmcnt(33)" ::: "memory"); break;
+    case 34: asm volatile("s_waitcnt vmcnt(34)" ::: "memory"); break;
+    case 35: asm volatile("s_waitcnt vmcnt(35)" ::: "memory"); break;
+    case 36: asm volatile("s_waitcnt vmcnt(36)" ::: "memory"); break;
+    case 37: asm volatile("s_waitcnt vmcnt(37)" ::: "memory"); break;
+    case 38: asm volatile("s_waitcnt vmcnt(38)" ::: "memory"); break;
+    case 39: asm volatile("s_waitcnt vmcnt(39)" ::: "memory"); break;
+    case 40: asm volatile("s_waitcnt vmcnt(40)" ::: "memory"); break;
     default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
     }
 }
@@ -259,6 +295,205 @@ k_router_seq(const float *__restrict__ x, int T, int K, int E, const float *__re
     if (my_t < T && my_e < E) logits[(int64_t)my_t * ldl + my_e] = acc;
 }
 
+// ---------------------------------------------------------------------------
+// Reference-order logits for few tokens.  Each logit is a chain of K
+// dependent fp32 additions, which is the whole latency when few tokens are
+// routed, so the multiplications leave the chain.  A workgroup of three waves
+// covers EPW experts x 4 tokens: waves 1-2 form the exact products
+// x[t][i]*W[e][i] of the next 128-wide chunk into an LDS product buffer while
+// wave 0 (lane EPW*t + e) adds the current chunk's products in order.  W and x
+// rows arrive by global_load_lds DMAs, issued by waves 1-2, through a ring of
+// RSM_RD stages.  EPW = 4 spreads one token's 128 rows over 32 workgroups,
+// EPW = 16 packs 4 tokens' work for more tokens.  Rows 16-byte aligned,
+// K % 4 == 0.
+// ---------------------------------------------------------------------------
+constexpr int RSM_CH = 128;                         // floats per chunk
+constexpr int RSM_RD = 8;                           // input ring stages (HBM latency at T = 1)
+constexpr int RSM_ROW = RSM_CH * 4;                 // input row bytes (unpadded)
+constexpr int RSM_PROWB = (RSM_CH + 4) * 4;         // product row bytes, padded
+constexpr int RSM_MAX_T = 32;                       // larger batches use k_router_seq
+template <int EPW> struct Rsm {
+    static constexpr int IN_ROWS = EPW + 4;         // EPW W rows + 4 x rows
+    static constexpr int NDMA = IN_ROWS / 4;        // DMAs per producer per chunk (2 rows each)
+    static constexpr int IN = IN_ROWS * RSM_ROW;    // ring stage bytes
+    static constexpr int P = 4 * EPW * RSM_PROWB;   // product buffer bytes
+    static constexpr int LDS = RSM_RD * IN + 2 * P;
+    static_assert(IN_ROWS % 4 == 0 && LDS <= 163840, "small router geometry");
+};
+
+__device__ __forceinline__ void lds_rd16(uint32_t a, u32x4 &v)
+{
+    asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a) : "memory");
+}
+
+__device__ __forceinline__ void lds_wr16(uint32_t a, const u32x4 &v)
+{
+    asm volatile("ds_write_b128 %0, %1" ::"v"(a), "v"(v) : "memory");
+}
+
+__device__ __forceinline__ void lds_wait_all()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
+// Block blk (16 products = 64 bytes) of a product row at LDS address pa.
+__device__ __forceinline__ void rsm_read(int blk, uint32_t pa, u32x4 (&v)[4])
+{
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v[i]) : "v"(pa), "i"(64 * blk + 16 * i) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void rsm_wait(u32x4 (&v)[4])
+{
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]) : "i"(N));
+}
+
+__device__ __forceinline__ void rsm_sum(float &acc, const u32x4 (&v)[4])
+{
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc = acc + __uint_as_float(v[i][j]);
+}
+
+__device__ void route_token(const RouteArgs &a, int t, int wv, int lane);
+
+template <int EPW>
+__global__ void __launch_bounds__(192)
+k_router_small(const float *__restrict__ x, int T, int K, int E, const float *__restrict__ w, int64_t wstride,
+               float *__restrict__ logits, int64_t ldl, RouteArgs topk, int *__restrict__ tickets)
+{
+#pragma clang fp contract(off)
+    using G = Rsm<EPW>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[G::LDS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t0 = blockIdx.x * 4, e0 = blockIdx.y * EPW;
+    const int nch = (K + RSM_CH - 1) / RSM_CH;
+    const uint32_t in0 = (uint32_t)(uintptr_t)(DS3_LDS void *)lds;
+    const uint32_t p0 = in0 + RSM_RD * G::IN;
+    const int pw = wave - 1;                        // producer index (waves 1, 2)
+
+    // producer pw moves input rows 2*NDMA*pw .. +2*NDMA-1, two per DMA
+    // (lanes 0-31 the first, 32-63 the second): rows 0..EPW-1 W (experts),
+    // then 4 x rows (tokens); rows past E / T repeat the last one (dropped)
+    const float *src[G::NDMA];
+#pragma unroll
+    for (int i = 0; i < G::NDMA; i++) {
+        const int r = 2 * (G::NDMA * pw + i) + (lane >> 5);
+        src[i] = r < EPW ? w + (int64_t)min(e0 + r, E - 1) * wstride : x + (int64_t)min(t0 + r - EPW, T - 1) * K;
+    }
+    auto issue = [&](int c) {
+        const uint32_t st = in0 + (uint32_t)((c % RSM_RD) * G::IN);
+        const int k = c * RSM_CH + 4 * (lane & 31);
+#pragma unroll
+        for (int i = 0; i < G::NDMA; i++) {
+            const float *p = src[i] + (k + 3 < K ? k : 0);      // past K: re-read the row start (unused)
+            __builtin_amdgcn_global_load_lds(
+                p, (DS3_LDS void *)(uintptr_t)(st + (uint32_t)(2 * (G::NDMA * pw + i) * RSM_ROW)), 16, 0, 0);
+        }
+    };
+    // products of chunk c into buffer b: lane l of producer pw handles float4
+    // k4 = l % 32 of experts 2pw + l/32 + 4s (s < EPW/4) for the 4 tokens;
+    // all reads are issued before one wait
+    auto produce = [&](int c, int b) {
+        const uint32_t st = in0 + (uint32_t)((c % RSM_RD) * G::IN), pb = p0 + (uint32_t)(b * G::P);
+        const int k4 = lane & 31, eb = 2 * pw + (lane >> 5);
+        u32x4 wv[EPW / 4], xv[4];
+#pragma unroll
+        for (int sj = 0; sj < EPW / 4; sj++) lds_rd16(st + (uint32_t)((eb + 4 * sj) * RSM_ROW + 16 * k4), wv[sj]);
+#pragma unroll
+        for (int tk = 0; tk < 4; tk++) lds_rd16(st + (uint32_t)((EPW + tk) * RSM_ROW + 16 * k4), xv[tk]);
+        lds_wait_all();
+#pragma unroll
+        for (int sj = 0; sj < EPW / 4; sj++)
+#pragma unroll
+            for (int tk = 0; tk < 4; tk++) {
+                u32x4 pr;
+#pragma unroll
+                for (int q = 0; q < 4; q++) pr[q] = __float_as_uint(__uint_as_float(xv[tk][q]) * __uint_as_float(wv[sj][q]));
+                lds_wr16(pb + (uint32_t)((EPW * tk + eb + 4 * sj) * RSM_PROWB + 16 * k4), pr);
+            }
+    };
+    // wait until this producer's DMAs of chunk c have landed: NDMA per chunk,
+    // chunks 0 .. issued-1 issued in order, so the NDMA * (issued - 1 - c)
+    // newest may stay in flight
+    int issued = 0;
+    auto wait_chunk = [&](int c) { rs_vm_wait(G::NDMA * (issued - 1 - c)); };
+
+    if (wave > 0) {
+        for (; issued < RSM_RD && issued < nch; issued++) issue(issued);
+        wait_chunk(0);
+    }
+    rs_barrier();
+    if (wave > 0) {
+        produce(0, 0);
+        if (nch > 1) wait_chunk(1);
+    }
+    rs_barrier();
+    float acc = 0.0f;
+    const bool chain = lane < 4 * EPW;
+    for (int c = 0; c < nch; c++) {
+        if (wave == 0) {
+            if (chain) {
+                const uint32_t pa = p0 + (uint32_t)((c & 1) * G::P + lane * RSM_PROWB);
+                const int kn = min(RSM_CH, K - c * RSM_CH);
+                if (kn == RSM_CH) {
+                    u32x4 v0[4], v1[4];
+                    rsm_read(0, pa, v0);
+#pragma unroll
+                    for (int blk = 0; blk < RSM_CH / 16; blk += 2) {
+                        rsm_read(blk + 1, pa, v1);
+                        rsm_wait<4>(v0);
+                        rsm_sum(acc, v0);
+                        if (blk + 2 < RSM_CH / 16) {
+                            rsm_read(blk + 2, pa, v0);
+                            rsm_wait<4>(v1);
+                        } else {
+                            rsm_wait<0>(v1);
+                        }
+                        rsm_sum(acc, v1);
+                    }
+                } else {
+                    for (int k = 0; k < kn; k++) {
+                        uint32_t v;
+                        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(pa + 4u * k) : "memory");
+                        acc = acc + __uint_as_float(v);
+                    }
+                }
+            }
+        } else {
+            if (c + 1 < nch) produce(c + 1, (c + 1) & 1);
+            if (c + RSM_RD < nch) {
+                issue(c + RSM_RD);                      // into the stage produce(c) read
+                issued++;
+            }
+            if (c + 2 < nch) wait_chunk(c + 2);
+        }
+        rs_barrier();
+    }
+    const int t = t0 + lane / EPW, e = e0 + lane % EPW;
+    if (wave == 0 && chain && t < T && e < E) logits[(int64_t)t * ldl + e] = acc;
+
+    // Fused top-k: the last of the gridDim.y workgroups of this token group to
+    // finish (a ticket per group, reset by that workgroup) routes its tokens
+    // from the logits all of them wrote; fences make the stores visible
+    // across XCDs before the ticket and to the reader after it.
+    if (topk.idx != nullptr) {
+        __shared__ int last_s;
+        __threadfence();
+        __syncthreads();
+        if (tid == 0) last_s = atomicAdd(&tickets[blockIdx.x], 1) == (int)gridDim.y - 1;
+        __syncthreads();
+        if (last_s) {
+            __threadfence();
+            for (int tt = t0 + wave; tt < min(t0 + 4, T); tt += 3) route_token(topk, tt, wave, lane);
+            if (tid == 0) tickets[blockIdx.x] = 0;
+        }
+    }
+}
+
 // Order-preserving map of finite floats (and infinities) to unsigned keys.
 __device__ __forceinline__ uint32_t order_key(float v)
 {
@@ -271,13 +506,10 @@ __device__ __forceinline__ float readlane_f(float v, int l)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
-__global__ void __launch_bounds__(256) k_route(RouteArgs a)
+// Softmax + top-k + renorm of token t by one wave (wv < 4: its LDS slot).
+__device__ void route_token(const RouteArgs &a, int t, int wv, int lane)
 {
-    const int lane = threadIdx.x & (WAVE - 1);
-    const int t = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
-    if (t >= a.T) return;                      // whole wave leaves together
     const int E = a.E;
-    const int wv = threadIdx.x / WAVE;
     const uint64_t below = (1ull << lane) - 1ull;
     __shared__ int cand_s[4][WAVE];
     __shared__ float val_s[4][WAVE];
@@ -420,6 +652,14 @@ __global__ void __launch_bounds__(256) k_route(RouteArgs a)
     }
 }
 
+__global__ void __launch_bounds__(256) k_route(RouteArgs a)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int t = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
+    if (t >= a.T) return;                      // whole wave leaves together
+    route_token(a, t, threadIdx.x / WAVE, lane);
+}
+
 bool router_seq_type_ok(int rtype, int K)
 {
     if (K <= 0) return false;
@@ -437,8 +677,10 @@ static void seq_launch(const float *x, int T, int K, int E, const float *w, int6
 }
 
 hipError_t launch_router_seq(const float *x, int T, int K, int E, int rtype, const uint8_t *rw, uint64_t rstride,
-                             float *wf32, float *logits, int64_t ldl, _Float16 *x16, hipStream_t s)
+                             float *wf32, float *logits, int64_t ldl, _Float16 *x16, const RouteArgs *topk,
+                             int *tickets, bool *topk_done, hipStream_t s)
 {
+    if (topk_done) *topk_done = false;
     if (T <= 0 || E <= 0 || E > ROUTE_MAX_E || !router_seq_type_ok(rtype, K)) return hipErrorInvalidValue;
     if (((uintptr_t)x & 3) != 0 || ((uintptr_t)x16 & 1) != 0) return hipErrorInvalidValue;
     const float *w = (const float *)rw;
@@ -464,7 +706,20 @@ hipError_t launch_router_seq(const float *x, int T, int K, int E, int rtype, con
     // 4 stages (3 chunks in flight) while one workgroup per CU covers the
     // tokens; 2 stages (two workgroups per CU) for long batches
     const bool deep = (T + 15) / 16 * ((E + 15) / 16) <= 512;
-    if (vec) {
+    RouteArgs none{};
+    if (vec && x16 == nullptr && T <= 4) {
+        // one token group: fuse top-k when the caller gave a ticket
+        const bool fuse = topk != nullptr && tickets != nullptr && topk->logits == logits &&
+                          topk->logit_stride == ldl && topk->T == T && topk->E == E;
+        const dim3 grid((unsigned)((T + 3) / 4), (unsigned)((E + 3) / 4));
+        hipLaunchKernelGGL(k_router_small<4>, grid, dim3(192), 0, s, x, T, K, E, w, wstride, logits, ldl,
+                           fuse ? *topk : none, tickets);
+        if (fuse && topk_done) *topk_done = true;
+    } else if (vec && x16 == nullptr && T <= RSM_MAX_T) {
+        const dim3 grid((unsigned)((T + 3) / 4), (unsigned)((E + 15) / 16));
+        hipLaunchKernelGGL(k_router_small<16>, grid, dim3(192), 0, s, x, T, K, E, w, wstride, logits, ldl, none,
+                           tickets);
+    } else if (vec) {
         if (deep) seq_launch<16, 4>(x, T, K, E, w, wstride, logits, ldl, x16, s);
         else seq_launch<16, 2>(x, T, K, E, w, wstride, logits, ldl, x16, s);
     } else {
