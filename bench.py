@@ -44,7 +44,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--tokens", type=int, default=512)
     p.add_argument("--layers", type=int, default=8, help="distinct resident layers cycled per step")
-    p.add_argument("--config", type=int, default=2, choices=(2, 3, 5))
+    p.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
+                   help="2, 3, 5: one layer on --tokens tokens (+ T=1 under t1); 4: the decode stack")
+    p.add_argument("--stack-layers", type=int, default=48, help="config 4: resident layers per decode step")
     p.add_argument("--t1-steps", type=int, default=200)
     p.add_argument("--no-t1", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
@@ -127,6 +129,8 @@ def run_gpu(args, T, steps, warmup, layers, xs, spec, n_used=8):
 
 
 def roofline(stats, spec, T, counts, n_used, traffic):
+    """traffic: {kernel: HBM bytes per launch} measured at T = 512, and at
+    T = 1 under "T1/<kernel>"."""
     name = next(iter(stats))                  # the one kernel timed in the timed region
     n, ms = stats[name]
     avg_s = ms / n / 1e3
@@ -135,8 +139,9 @@ def roofline(stats, spec, T, counts, n_used, traffic):
     r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
          "kernel_avg_us": round(avg_s * 1e6, 2), "alg_bytes_per_launch": b}
-    if traffic and name in traffic:
-        r["traffic"] = traffic[name]
+    key = ("T1/" if T == 1 else "") + name
+    if traffic and key in traffic and T in (1, 512):
+        r["traffic"] = traffic[key]
     return r
 
 
@@ -188,6 +193,88 @@ def cpu_baseline(layer, x, n_used, n_tokens):
                       f"resident, ds3_ref_moe_ffn per token on {threads} threads ({dt:.1f}s wall)"}
 
 
+def run_stack(args, n_used=8):
+    """Configuration 4: one token per step through a resident stack of
+    --stack-layers MoE layers, h <- h + MoE_l(h) (output zeroed, then the
+    residual fused into the call), as the engine runs decode.  Returns the
+    JSON line."""
+    from qw3_amd import ds3
+    from qw3_amd import workload as W
+    from qw3_amd._native import hip
+    spec = W.config_spec(4)
+    L, K, E = args.stack_layers, spec.n_embd, spec.n_expert
+    t0 = time.perf_counter()
+    layers = [W.make_layer(spec, seed=1234, layer=l).to_device() for l in range(L)]
+    log(f"[bench] config 4: {L} layers generated and resident in {time.perf_counter() - t0:.1f}s "
+        f"({L * (W.expert_bytes(spec) * E + W.router_bytes(spec)) / 2**30:.2f} GiB)")
+    hs = [ds3.Buffer.from_array(W.make_inputs(4, 1, seed=99, step=s)) for s in range(8)]
+    bufs = [ds3.Buffer.alloc(K * 4) for _ in range(2)]
+    idx = ds3.Buffer.alloc(n_used * 4)
+
+    def token(i, want_idx=False):
+        src = hs[i % len(hs)]
+        for l, d in enumerate(layers):
+            dst = bufs[l & 1]
+            dst.zero()
+            ds3.moe_ffn_batch(src, d.router, spec.router_type, d.experts, dst, 1, E, n_used, residual=src,
+                              indices=idx if (want_idx and l == 0) else None)
+            src = dst
+
+    token(0, want_idx=True)
+    hip().ds3_hip_synchronize()
+    counts = np.bincount(idx.read(np.int32, (n_used,)), minlength=E)
+    hip().ds3_hip_kernel_timing_only(None)
+    hip().ds3_hip_kernel_timing_reset()
+    hip().ds3_hip_kernel_timing(1)
+    hip().ds3_hip_begin_batch()
+    for i in range(1, args.warmup + 1):
+        token(i)
+    hip().ds3_hip_end_batch()
+    hip().ds3_hip_kernel_timing(0)
+    brk = ds3.kernel_stats()
+    dominant = max((k for k in brk if kernel_bytes(k, spec, 1, counts, n_used) is not None),
+                   key=lambda k: brk[k][1])
+    hip().ds3_hip_kernel_timing_reset()
+    hip().ds3_hip_kernel_timing_only(dominant.encode())
+    hip().ds3_hip_kernel_timing(1)
+    hip().ds3_hip_synchronize()
+    hip().ds3_hip_begin_batch()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        token(i)
+    hip().ds3_hip_end_batch()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    hip().ds3_hip_kernel_timing(0)
+    hip().ds3_hip_kernel_timing_only(None)
+    stats = ds3.kernel_stats()
+    ms = wall_ms / args.steps
+    log(f"[bench] config 4: {ms * 1e3:.1f} us/token through {L} layers ({ms * 1e3 / L:.2f} us/layer)")
+    log_breakdown(brk, stats)
+    b = L * W.algorithmic_bytes(spec, 1, n_used)
+    tpath = Path(args.traffic) if args.traffic else ROOT / "profiles" / "hbm_traffic.json"
+    traffic = json.loads(tpath.read_text()) if tpath.exists() else None
+    return {
+        "metric": f"decode tokens/s through a {L}-layer resident MoE-FFN stack (configs[3]); HBM GB/s vs peak",
+        "value": round(1 / (ms / 1e3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded generator; expert weights N(0,0.02) quantised by this project's GGUF quantisers)",
+        "config": {"workload": f"configs[3]: decode, one token through {L} resident Qwen3-30B-A3B MoE-FFN layers, "
+                               f"h <- h + MoE_l(h); Q4_K gate/up + Q6_K down, F32 router",
+                   "tokens": 1, "layers": L, "n_embd": K, "n_ff": spec.n_ff},
+        "roofline": roofline(stats, spec, 1, counts, n_used, traffic),
+        "alg_bytes_per_step": b,
+        "hbm_frac_step": round(b / (ms / 1e3) / (HBM_PEAK_GBS * 1e9), 4),
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -210,6 +297,9 @@ def main():
         log(f"[bench] copy calibration: 3 x {args.copy_mib} MiB device copy")
         a.close()
         b.close()
+    if args.config == 4:
+        print(json.dumps(run_stack(args)), flush=True)
+        return
     spec = W.config_spec(args.config)
     T, n_used = args.tokens, W.N_USED
     t0 = time.perf_counter()

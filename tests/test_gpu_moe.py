@@ -322,6 +322,25 @@ def test_residual_and_accumulate(hip_ready, real):
         assert_close(got - res, want, max_abs=3e-3, rel_l2=1.2e-3)
 
 
+def test_decode_stack_teacher_forced_config4(hip_ready):
+    """Configuration 4 in small: h <- h + MoE_l(h) through distinct layers at
+    T = 1 (decode path, residual fused), each layer checked against the
+    oracle on the oracle's own input (teacher forcing), for a few steps of
+    fresh tokens."""
+    spec = W.config_spec(4)
+    cases = [Case(spec, seed=1234, layer=l) for l in range(3)]
+    for step in range(2):
+        h = W.make_inputs(4, 1, seed=99, step=step)
+        for l, case in enumerate(cases):
+            want, oi, _, probs = case.oracle(h)
+            want = want + h                                 # residual (reference src/ds3_reference.c:455-460)
+            print(f"  stack step {step} layer {l}", flush=True)
+            got, gi, _, _ = case.gpu_batch(h, residual=h)
+            assert index_mismatches(gi, oi, probs) == 0
+            assert_close(got, want, max_abs=3e-3, rel_l2=1.2e-3)
+            h = want                                        # teacher forcing
+
+
 # ---------------------------------------------------------------------------
 # ds3_metal.h entry points (reference tests/test_moe_metal.c cases)
 # ---------------------------------------------------------------------------
