@@ -128,7 +128,10 @@ int ds3_hip_silu_mul_f32(const ds3_hip_buffer_t *gate, const ds3_hip_buffer_t *u
 
 /* reference src/ds3_metal.h:340-374 (one token).  output accumulates
  * (caller zeroes it).  expert_offsets: optional [n_expert][3] uint64 byte
- * offsets {gate, up, down}; when NULL expert e starts at e*rows*row_stride. */
+ * offsets {gate, up, down}; when NULL expert e starts at e*rows*row_stride.
+ * Routing uses the certified router (see ds3_hip_set_router_mode): the
+ * selected experts are the reference's; gate_logits are within a proven
+ * bound of the reference's sequential fp32 sums. */
 int ds3_hip_moe_ffn(
     const ds3_hip_buffer_t *input, const ds3_hip_buffer_t *w_gate_inp,
     const ds3_hip_buffer_t *w_gate_exps, const ds3_hip_buffer_t *w_up_exps, const ds3_hip_buffer_t *w_down_exps,
@@ -195,7 +198,12 @@ void ds3_hip_profile_print(const char *label);
  *   input [T][n_embd] f32; output [T][n_embd] f32 accumulates (caller
  *   zeroes); residual (optional) [T][n_embd] is added to output;
  *   indices / scores (optional) receive the routing [T][n_used];
- *   gate_logits (optional) receives the logits [T][n_expert]. */
+ *   gate_logits (optional) receives the logits [T][n_expert].
+ * Up to 64 tokens (see ds3_hip_set_router_mode) the router is the certified
+ * one: indices equal the reference's; gate_logits hold the fp32 rounding of
+ * the exact sum of the reference's fp32 products (the reference's own
+ * sequential sums for experts whose order needed them), within a proven
+ * bound of the reference's logits. */
 int ds3_hip_moe_ffn_batch(
     const ds3_hip_buffer_t *input, const ds3_hip_buffer_t *w_gate_inp,
     const ds3_hip_buffer_t *w_gate_exps, const ds3_hip_buffer_t *w_up_exps, const ds3_hip_buffer_t *w_down_exps,
@@ -225,6 +233,20 @@ int ds3_hip_moe_bucket(const ds3_hip_buffer_t *indices, const ds3_hip_buffer_t *
  * (the parity probe for the block decoders). */
 int ds3_hip_dequantize(const ds3_hip_buffer_t *src, uint64_t src_offset, ds3_hip_type_t type, uint64_t n,
                        ds3_hip_buffer_t *dst);
+
+/* Router selection.  0 (default): the certified router (fp64 wavefront sums
+ * with a proven error bound, exact sequential sums only where the bound
+ * cannot certify the top-k order) in ds3_hip_moe_ffn and, up to 64 tokens,
+ * in ds3_hip_moe_ffn_batch; the reference's sequential-order sums (logits
+ * bit-identical to the reference's) everywhere else.  1: sequential-order
+ * sums everywhere.  2: the certified router wherever its shape limits allow
+ * (n_embd a multiple of 256 up to 4096), ds3_hip_moe_route included.
+ * Returns the previous mode. */
+int ds3_hip_set_router_mode(int mode);
+
+/* Tokens the certified router has certified / repaired (exact sequential
+ * sums for some candidates) since init or the last reset; synchronises. */
+int ds3_hip_router_stats(uint64_t *certified, uint64_t *repaired, int reset);
 
 /* ds3_hip_moe_ffn_batch uses the grouped (prefill) path when
  * n_tokens >= min_tokens, the per-token GEMV path otherwise.  0 restores the

@@ -29,6 +29,8 @@ using namespace ds3k;
 namespace {
 
 constexpr int kDefaultPrefillMin = 16;
+constexpr int kTickets = 32;             // router token-group tickets (zero between launches)
+constexpr int kCertMaxTokens = 64;       // automatic mode: certified router up to this many tokens
 constexpr size_t kAllocPad = 256;        // slack after every allocation: kernels read whole dwords
 
 struct KRec {
@@ -43,7 +45,9 @@ struct State {
     uint8_t *ws = nullptr;
     size_t ws_bytes = 0;
     int32_t *zero_idx = nullptr;     // device {0}
-    int32_t *tickets = nullptr;      // 32 router tickets (zero between launches)
+    int32_t *tickets = nullptr;      // kTickets router tickets (zero between launches)
+    int router_mode = 0;             // ds3_hip_set_router_mode
+    unsigned long long *cert_stats = nullptr;   // device {certified, repaired} token counts
     float *one_f = nullptr;          // device {1.0f}
     int prefill_min = kDefaultPrefillMin;
     // reference-style profiling (src/ds3_metal.m:2868-2885)
@@ -235,11 +239,13 @@ extern "C" int ds3_hip_init(void)
         return -1;
     }
     void *consts = nullptr;
-    if (hipMalloc(&consts, 256) != hipSuccess) return -1;
+    if (hipMalloc(&consts, 128 + (size_t)kTickets * 4 + 16) != hipSuccess) return -1;
     g.zero_idx = (int32_t *)consts;
     g.one_f = (float *)((uint8_t *)consts + 64);
     g.tickets = (int32_t *)((uint8_t *)consts + 128);   // router token-group tickets, kept at zero between launches
-    if (hipMemsetAsync(g.tickets, 0, 128, g.stream) != hipSuccess || hipStreamSynchronize(g.stream) != hipSuccess)
+    g.cert_stats = (unsigned long long *)((uint8_t *)consts + 128 + (size_t)kTickets * 4);
+    if (hipMemsetAsync(g.tickets, 0, (size_t)kTickets * 4 + 16, g.stream) != hipSuccess ||
+        hipStreamSynchronize(g.stream) != hipSuccess)
         return -1;
     const int32_t zi = 0;
     const float one = 1.0f;
@@ -597,19 +603,20 @@ struct RouteBufs {
     float *scores;
     float *wf32;         // [E][n_embd] FP32 copy of router rows stored in another type
     _Float16 *x16;       // optional [T][n_embd] fp16 copy of x, written by the router
+    void *cert;          // certified router scratch (router_cert_scratch bytes)
 };
 
 // Scratch of route_tokens beyond the output buffers, laid out from `base`.
 struct RouteScratch {
-    size_t o_wf32, bytes;
+    size_t o_wf32, o_cert, bytes;
 };
 
 RouteScratch route_scratch(int T, uint32_t n_embd, uint32_t n_expert)
 {
-    (void)T;
     Bump b;
     RouteScratch r;
     r.o_wf32 = b.take((size_t)n_expert * n_embd * 4);
+    r.o_cert = b.take(router_cert_scratch(T, (int)n_expert));
     r.bytes = b.off;
     return r;
 }
@@ -617,13 +624,25 @@ RouteScratch route_scratch(int T, uint32_t n_embd, uint32_t n_expert)
 RouteBufs route_bufs(uint8_t *base, const RouteScratch &r, float *logits, int32_t *idx, float *scores,
                      _Float16 *x16)
 {
-    return RouteBufs{ logits, idx, scores, (float *)(base + r.o_wf32), x16 };
+    return RouteBufs{ logits, idx, scores, (float *)(base + r.o_wf32), x16, base + r.o_cert };
+}
+
+// Whether the certified router serves this call: entry points that only need
+// the routing (allow) take it for few tokens, or always under router mode 2;
+// mode 1 keeps the sequential-order router everywhere.
+bool use_cert(const float *x, int T, uint32_t n_embd, uint32_t n_expert, uint32_t n_used, bool allow)
+{
+    if (g.router_mode == 1 || !router_cert_ok((int)n_embd, (int)n_expert, (int)n_used)) return false;
+    if (((uintptr_t)x & 15) != 0) return false;
+    if (g.router_mode == 2) return true;
+    return allow && T <= kCertMaxTokens;
 }
 
 // Router logits + softmax/top-k/renorm for T tokens.  Sets *x16_done when the
 // router also wrote rb.x16.
 int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstride, int rtype, int T, uint32_t n_embd,
-                 uint32_t n_expert, uint32_t n_used, bool norm, const RouteBufs &rb, bool *x16_done = nullptr)
+                 uint32_t n_expert, uint32_t n_used, bool norm, const RouteBufs &rb, bool *x16_done = nullptr,
+                 bool allow_cert = false)
 {
     RouteArgs ra{};
     ra.logits = rb.logits;
@@ -636,6 +655,15 @@ int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstrid
     ra.out_stride = n_used;
     ra.norm = norm;
     hipError_t e;
+    if (use_cert(x, T, n_embd, n_expert, n_used, allow_cert)) {
+        {
+            KScope ks("router_logits");
+            e = launch_router_cert(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, rb.wf32,
+                                   rb.logits, n_expert, rb.x16, ra, rb.cert, g.cert_stats, g.stream);
+        }
+        if (x16_done) *x16_done = rb.x16 != nullptr;
+        return report(e, "router (certified)");
+    }
     bool topk_done = false;
     {
         KScope ks("router_logits");
@@ -714,7 +742,7 @@ extern "C" int ds3_hip_moe_ffn(
     const float *x = fptr(input);
     const RouteBufs rb = route_bufs(ws + o_r, rs, fptr(gate_logits), idx, sc, nullptr);
     if (route_tokens(x, w_gate_inp, router_row_stride, router_type, 1, n_embd, n_expert, n_used, norm_topk_prob,
-                     rb) != 0)
+                     rb, nullptr, true) != 0)
         return -1;
     if (has_shared &&
         run_shared(x, w_shared_gate, w_shared_up, w_shared_down, shared_gate_type, shared_up_type, shared_down_type,
@@ -973,7 +1001,7 @@ extern "C" int ds3_hip_moe_ffn_batch(
     const float *x = fptr(input);
     bool x16_done = false;
     if (route_tokens(x, w_gate_inp, router_row_stride, router_type, (int)T, n_embd, n_expert, n_used, norm_topk_prob,
-                     rb, &x16_done) != 0)
+                     rb, &x16_done, true) != 0)
         return -1;
     ExpertWeights ew = make_ew(w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type, down_type, gate_row_stride,
                                up_row_stride, down_row_stride, expert_offsets);
@@ -1047,6 +1075,28 @@ extern "C" int ds3_hip_dequantize(const ds3_hip_buffer_t *src, uint64_t src_offs
     if (!fits(src, src_offset + n / blk * bytes, "src") || !fits(dst, n * 4, "dst")) return -1;
     KScope ks("dequant");
     return finish(launch_dequant(type, cptr(src) + src_offset, fptr(dst), (int64_t)n, g.stream), "dequantize");
+}
+
+extern "C" int ds3_hip_router_stats(uint64_t *certified, uint64_t *repaired, int reset)
+{
+    if (!ensure_init()) return -1;
+    unsigned long long v[2] = { 0, 0 };
+    if (hipStreamSynchronize(g.stream) != hipSuccess ||
+        hipMemcpy(v, g.cert_stats, sizeof v, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    if (certified) *certified = v[0];
+    if (repaired) *repaired = v[1];
+    if (reset && (launch_fill_zero((float *)g.cert_stats, 4, g.stream) != hipSuccess ||
+                  hipStreamSynchronize(g.stream) != hipSuccess))
+        return -1;
+    return 0;
+}
+
+extern "C" int ds3_hip_set_router_mode(int mode)
+{
+    const int prev = g.router_mode;
+    g.router_mode = (mode >= 0 && mode <= 2) ? mode : 0;
+    return prev;
 }
 
 extern "C" int ds3_hip_set_prefill_min_tokens(int min_tokens)

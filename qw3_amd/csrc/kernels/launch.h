@@ -29,11 +29,6 @@ hipError_t launch_gemv(int type, const float *A, int64_t lda, const uint8_t *w, 
 
 bool gemv_type_ok(int type, int K);
 
-// Router logits in the reference's order: logits[t][e] (row stride ldl) =
-// x[t][0]*W[e][0] + x[t][1]*W[e][1] + ... summed left to right with every
-// product and sum rounded to fp32, bit-identical to the reference's.  Router
-// rows of any supported type (F32 / F16 / Q8_0 / Q4_K / Q6_K) at rw, rstride
-// bytes apart; rows other than 4-byte aligned F32 are first expanded into
 // Router tail: logits [T][E] -> softmax -> top-k -> renorm, selected by
 // (prob desc, index asc) like the reference.
 struct RouteArgs {
@@ -47,6 +42,11 @@ struct RouteArgs {
 };
 hipError_t launch_route(const RouteArgs &a, hipStream_t s);
 
+// Router logits in the reference's order: logits[t][e] (row stride ldl) =
+// x[t][0]*W[e][0] + x[t][1]*W[e][1] + ... summed left to right with every
+// product and sum rounded to fp32, bit-identical to the reference's.  Router
+// rows of any supported type (F32 / F16 / Q8_0 / Q4_K / Q6_K) at rw, rstride
+// bytes apart; rows other than 4-byte aligned F32 are first expanded into
 // wf32 [E][K].  If x16 != nullptr also x16[t][k] = (fp16) x[t][k].  E <= 256;
 // K a whole number of blocks of rtype.  With topk (describing these logits)
 // and tickets (zeroed device ints, left zeroed) the kernel may also run the
@@ -55,6 +55,21 @@ bool router_seq_type_ok(int rtype, int K);
 hipError_t launch_router_seq(const float *x, int T, int K, int E, int rtype, const uint8_t *rw, uint64_t rstride,
                              float *wf32, float *logits, int64_t ldl, _Float16 *x16, const RouteArgs *topk,
                              int *tickets, bool *topk_done, hipStream_t s);
+
+// Certified router for few tokens (two launches): fp64 wavefront sums of the
+// reference's fp32 products with a proven bound on the reference's
+// sequential-sum error, then a selection that certifies the top-k order
+// against the bounds; tokens it cannot certify get the exact sequential
+// logits of their candidate experts before selection.  Indices equal the
+// reference's; logits are fl32 of the fp64 sums (the exact chains for
+// repaired candidates).  ra must describe these logits; scratch:
+// router_cert_scratch(T, E) bytes, 8-byte aligned; x, x16 16-byte aligned.
+// stats (optional): device counters {tokens certified, tokens repaired}.
+bool router_cert_ok(int K, int E, int k);
+size_t router_cert_scratch(int T, int E);
+hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, const uint8_t *rw, uint64_t rstride,
+                              float *wf32, float *logits, int64_t ldl, _Float16 *x16, const RouteArgs &ra,
+                              void *scratch, unsigned long long *stats, hipStream_t s);
 
 // Decode (small T) expert products.
 //   h[slot][F] = silu(x[t] . Wg_e) * (x[t] . Wu_e), slot = t*n_used + k, e = idx[slot]

@@ -660,6 +660,566 @@ __global__ void __launch_bounds__(256) k_route(RouteArgs a)
     route_token(a, t, threadIdx.x / WAVE, lane);
 }
 
+// ---------------------------------------------------------------------------
+// Certified router (latency path for few tokens).
+//
+// The reference's logit is a chain of K dependent fp32 additions
+// (src/ds3_reference.c:424-434): ~K * 6 cycles of latency however many lanes
+// are free.  Instead, for each (token, expert):
+//   S = sum_i p_i in fp64, where p_i = fl32(x_i * w_i) are the reference's
+//       own rounded products (exact in fp64), and
+//   B >= |reference logit - S|, a proven bound.  The reference's k-th partial
+//       sum rounds once, |s^_k - (s^_{k-1} + p_k)| <= u |s^_k| (u = 2^-24), so
+//       |s^_K - s_K| <= u sum_k |s^_k| <= u A / (1 - K u), A = sum_k |s_k|
+//       over the exact prefix sums s_k of the p_i.  A is evaluated from the
+//       same products (lane-local prefixes, a wavefront scan, the workgroup's
+//       wave totals) and inflated by a bound on its own rounding; the host
+//       folds every constant into bfac (router_cert_bfac):
+//       B = bfac * A_computed + 1e-35.
+// k_router_sums: one workgroup per (token group, expert), each of its 4
+// waves sums a quarter of K, so one memory round trip brings every operand.
+// k_router_select: one workgroup per token group ranks the experts by
+// (fl32(S) desc, index asc), then certifies the top k: every adjacent pair
+// in that order, and the k-th against every other expert, must be separated
+// by more than B_a + B_b + tau, where tau covers the reference's softmax
+// roundings (l - max, expf, the normalisation; src/ds3_reference.c:344-359)
+// so that its probabilities order the same way, strictly.  A certified
+// token's top k, in order, is the reference's, and its weights come from
+// the fl32(S) logits.  A token that fails (about 2 % at N(0, 0.02) routers)
+// is repaired: every expert that could still reach the top k gets the
+// reference's exact sequential chain, then the ordinary selection runs on
+// the repaired row.
+// ---------------------------------------------------------------------------
+constexpr int RC_WAVES = 4;
+constexpr int RC_THREADS = 64 * RC_WAVES;
+
+struct CertArgs {
+    double *S;                   // [T][E]
+    float *B;                    // [T][E]
+    float bfac;
+    int nb;                      // candidate rows per repair batch (dynamic LDS rows of K + 4 floats)
+    unsigned long long *stats;   // optional [2]: tokens certified, tokens repaired
+};
+
+// DPP lane moves: row_shr:n inside rows of 16 lanes, row_bcast:15 / :31,
+// wave_shr:1.  Lanes without a source lane read 0.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ double dpp_d(double v)
+{
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROW_MASK, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROW_MASK, 0xf, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Inclusive prefix sum over the wavefront: four row_shr steps inside each
+// row of 16, then rows 1 and 3 add lane 15 of the row below, rows 2 and 3
+// lane 31.  Every result is a tree of at most 6 additions.
+__device__ __forceinline__ float wave_incl_scan(float v)
+{
+    v = v + dpp_f<0x111>(v);
+    v = v + dpp_f<0x112>(v);
+    v = v + dpp_f<0x114>(v);
+    v = v + dpp_f<0x118>(v);
+    v = v + dpp_f<0x142, 0xa>(v);
+    v = v + dpp_f<0x143, 0xc>(v);
+    return v;
+}
+
+__device__ __forceinline__ double wave_incl_scan_f64(double v)
+{
+    v = v + dpp_d<0x111>(v);
+    v = v + dpp_d<0x112>(v);
+    v = v + dpp_d<0x114>(v);
+    v = v + dpp_d<0x118>(v);
+    v = v + dpp_d<0x142, 0xa>(v);
+    v = v + dpp_d<0x143, 0xc>(v);
+    return v;
+}
+
+__device__ __forceinline__ double readlane_d(double v, int l)
+{
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Spacing of fp32 numbers at magnitude m: 2^(e - 23) for m in [2^e, 2^(e+1)).
+__device__ __forceinline__ double f32_ulp(double m)
+{
+    const float f = (float)fmax(m, 1e-30);
+    return (double)ldexpf(1.0f, ilogbf(f) - 23);
+}
+
+// Order-preserving unsigned key of a double (larger value, larger key).
+__device__ __forceinline__ unsigned long long order_key_d(double v)
+{
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    return (u & 0x8000000000000000ull) ? ~u : (u | 0x8000000000000000ull);
+}
+
+// L contiguous floats at p (16-, 8- or 4-byte loads as L allows).
+template <int L>
+__device__ __forceinline__ void load_run(const float *p, float (&v)[L])
+{
+    if constexpr (L % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < L; i += 4) {
+            const float4 q = *(const float4 *)(p + i);
+            v[i] = q.x; v[i + 1] = q.y; v[i + 2] = q.z; v[i + 3] = q.w;
+        }
+    } else if constexpr (L % 2 == 0) {
+#pragma unroll
+        for (int i = 0; i < L; i += 2) {
+            const float2 q = *(const float2 *)(p + i);
+            v[i] = q.x; v[i + 1] = q.y;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < L; i++) v[i] = p[i];
+    }
+}
+
+// S, B and fl32(S) for TG tokens x one expert.  Lane l of wave w covers
+// elements (64 w + l) L .. + L - 1, K = 256 L.
+template <int L, int TG>
+__global__ void __launch_bounds__(RC_THREADS)
+k_router_sums(const float *__restrict__ x, int T, int K, int E, const float *__restrict__ w, int64_t wstride,
+              float *__restrict__ logits, int64_t ldl, _Float16 *__restrict__ x16, CertArgs ca)
+{
+#pragma clang fp contract(off)
+    __shared__ float tot_s[TG][RC_WAVES];
+    __shared__ float am_s[TG][RC_WAVES];
+    __shared__ double sum_s[TG][RC_WAVES];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t0 = blockIdx.x * TG, e = blockIdx.y;
+    const int k0 = tid * L;
+    float wv[L], pv[TG][L];
+    load_run<L>(w + (int64_t)e * wstride + k0, wv);
+#pragma unroll
+    for (int tt = 0; tt < TG; tt++) load_run<L>(x + (int64_t)min(t0 + tt, T - 1) * K + k0, pv[tt]);
+    if (x16 != nullptr && blockIdx.y == 0) {
+#pragma unroll
+        for (int tt = 0; tt < TG; tt++) {
+            if (t0 + tt >= T) continue;
+            _Float16 *d = x16 + (int64_t)(t0 + tt) * K + k0;
+#pragma unroll
+            for (int i = 0; i < L; i++) d[i] = (_Float16)pv[tt][i];
+        }
+    }
+    double sl[TG];
+    float ex[TG];
+#pragma unroll
+    for (int tt = 0; tt < TG; tt++) {
+        double s = 0.0;
+        float r = 0.0f;
+#pragma unroll
+        for (int i = 0; i < L; i++) {
+            const float p = pv[tt][i] * wv[i];      // the reference's rounded product
+            s += (double)p;
+            r = r + p;
+            pv[tt][i] = r;                          // lane-local prefix
+        }
+        sl[tt] = s;
+        // exclusive prefix of the lane totals, and the wave total
+        ex[tt] = wave_incl_scan(dpp_f<0x138>(r));
+        const float tot = readlane_f(ex[tt], 63) + readlane_f(r, 63);
+        if (lane == 0) tot_s[tt][wave] = tot;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int tt = 0; tt < TG; tt++) {
+        float wbase = 0.0f;
+        for (int v = 0; v < wave; v++) wbase = wbase + tot_s[tt][v];
+        const float base = wbase + ex[tt];
+        float am = 0.0f;
+#pragma unroll
+        for (int i = 0; i < L; i++) am = am + fabsf(base + pv[tt][i]);
+        am = readlane_f(wave_incl_scan(am), 63);
+        const double s = readlane_d(wave_incl_scan_f64(sl[tt]), 63);
+        if (lane == 0) {
+            am_s[tt][wave] = am;
+            sum_s[tt][wave] = s;
+        }
+    }
+    __syncthreads();
+    if (tid < TG && t0 + tid < T) {
+        const int t = t0 + tid;
+        double s = sum_s[tid][0];
+        float am = am_s[tid][0];
+#pragma unroll
+        for (int v = 1; v < RC_WAVES; v++) {
+            s = s + sum_s[tid][v];
+            am = am + am_s[tid][v];
+        }
+        ca.S[(int64_t)t * E + e] = s;
+        ca.B[(int64_t)t * E + e] = am * ca.bfac + 1e-35f;
+        logits[(int64_t)t * ldl + e] = (float)s;
+    }
+}
+
+// Emit the k selected experts of a token from its fp32 logits (l: this
+// lane's experts lane + 64 j) in the order given by (my_e, my_v) of lanes
+// 0..k-1: the reference's softmax over all E logits, top-k values,
+// renormalisation (src/ds3_reference.c:344-359, 632-639).
+__device__ __forceinline__ void emit_ranked(const RouteArgs &a, int t, const float (&l)[ROUTE_EPL], float my_v,
+                                            float mx, int my_e, int lane)
+{
+    const int E = a.E;
+    float sp = 0.f;
+#pragma unroll
+    for (int j = 0; j < ROUTE_EPL; j++)
+        if (lane + WAVE * j < E) sp += expf(l[j] - mx);
+    const float inv = 1.0f / wave_sum(sp);
+    const float p = expf(my_v - mx) * inv;
+    float ssum = 0.f;
+    for (int r = 0; r < a.k; r++) ssum += readlane_f(p, r);     // sequential, in k order
+    if (lane < a.k) {
+        float wt = p;
+        if (a.norm && ssum > 0.0f) wt *= 1.0f / ssum;
+        a.idx[(int64_t)t * a.out_stride + lane] = my_e;
+        a.scores[(int64_t)t * a.out_stride + lane] = wt;
+    }
+}
+
+// Exact reference chains for the candidate experts of token t (the whole
+// workgroup): the products of nb candidates at a time go to LDS, then lane m
+// of wave 0 adds candidate m's in order and overwrites its logit.
+__device__ void cert_repair(const float *__restrict__ x, int K, const float *__restrict__ w, int64_t wstride,
+                            int t, const uint64_t (&cand)[4], float *logits_row, int nb, float *prod)
+{
+#pragma clang fp contract(off)
+    __shared__ int list_s[ROUTE_MAX_E];
+    __shared__ int n_s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    {
+        const uint64_t m = cand[wave];
+        int pre = 0;
+        for (int j = 0; j < wave; j++) pre += __popcll(cand[j]);
+        if ((m >> lane) & 1ull) list_s[pre + __popcll(m & ((1ull << lane) - 1ull))] = tid;
+        if (tid == 0) n_s = __popcll(cand[0]) + __popcll(cand[1]) + __popcll(cand[2]) + __popcll(cand[3]);
+    }
+    __syncthreads();
+    const int n = n_s;
+    const int rowf = K + 4;
+    const float *xr = x + (int64_t)t * K;
+    for (int b0 = 0; b0 < n; b0 += nb) {
+        const int nbb = min(nb, n - b0);
+        for (int m = wave; m < nbb; m += RC_WAVES) {
+            const float *wr = w + (int64_t)list_s[b0 + m] * wstride;
+            for (int i = 4 * lane; i < K; i += 4 * WAVE) {
+                const float4 wq = *(const float4 *)(wr + i), xq = *(const float4 *)(xr + i);
+                float4 p;
+                p.x = xq.x * wq.x;
+                p.y = xq.y * wq.y;
+                p.z = xq.z * wq.z;
+                p.w = xq.w * wq.w;
+                *(float4 *)(prod + (int64_t)m * rowf + i) = p;
+            }
+        }
+        __syncthreads();
+        if (tid < nbb) {
+            const float *pr = prod + (int64_t)tid * rowf;
+            float acc = 0.0f;
+            for (int i = 0; i < K; i += 16) {
+                float4 v[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) v[q] = *(const float4 *)(pr + i + 4 * q);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    acc = acc + v[q].x;
+                    acc = acc + v[q].y;
+                    acc = acc + v[q].z;
+                    acc = acc + v[q].w;
+                }
+            }
+            logits_row[list_s[b0 + tid]] = acc;
+        }
+        __syncthreads();
+    }
+}
+
+// Rank, certify, emit (and repair) the routing of TG tokens.
+template <int TG>
+__global__ void __launch_bounds__(RC_THREADS)
+k_router_select(const float *__restrict__ x, int K, const float *__restrict__ w, int64_t wstride, CertArgs ca,
+                RouteArgs a)
+{
+    extern __shared__ __attribute__((aligned(16))) float rc_prod[];
+    __shared__ double sS[TG][ROUTE_MAX_E];
+    __shared__ float sB[TG][ROUTE_MAX_E];
+    __shared__ __attribute__((aligned(16))) unsigned long long key_s[TG][ROUTE_MAX_E];
+    __shared__ int rank_s[TG][ROUTE_MAX_E];
+    __shared__ uint8_t sel_s[TG][ROUTE_MAX_E];
+    __shared__ int ord_s[TG][WAVE];
+    __shared__ unsigned int bmax_s[TG];
+    __shared__ unsigned long long smax_s[TG], hi_s[TG];
+    __shared__ int bad_s[TG], fail_s[TG];
+    __shared__ uint64_t cand_s[TG][4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int E = a.E, k = a.k, T = a.T;
+    const int t0 = blockIdx.x * TG;
+    constexpr int PER = (TG * ROUTE_MAX_E + RC_THREADS - 1) / RC_THREADS;
+    const int E32 = (E + 31) & ~31;             // key rows padded with zero keys (below every expert)
+    if (tid < TG) {
+        bmax_s[tid] = 0u;
+        smax_s[tid] = 0ull;
+        hi_s[tid] = 0ull;                   // below every key: no other expert
+        bad_s[tid] = 0;
+        fail_s[tid] = 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < PER; r++) {
+        const int p = tid + RC_THREADS * r, tt = p / E, e = p - tt * E;
+        if (tt >= TG || t0 + tt >= T) continue;
+        const double s = ca.S[(int64_t)(t0 + tt) * E + e];
+        const float b = ca.B[(int64_t)(t0 + tt) * E + e];
+        const float lf = (float)s;
+        sS[tt][e] = s;
+        sB[tt][e] = b;
+        sel_s[tt][e] = 0;
+        rank_s[tt][e] = 0;
+        key_s[tt][e] = ((unsigned long long)order_key(lf) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)e);
+        if (!__builtin_isfinite(s) || !__builtin_isfinite(b) || !__builtin_isfinite(lf)) bad_s[tt] = 1;
+        atomicMax(&bmax_s[tt], __float_as_uint(b));
+        atomicMax(&smax_s[tt], __builtin_bit_cast(unsigned long long, fabs(s)));
+    }
+    __syncthreads();
+    if (E32 > E)
+        for (int q = tid; q < TG * (E32 - E); q += RC_THREADS) key_s[q / (E32 - E)][E + q % (E32 - E)] = 0ull;
+    __syncthreads();
+    // rank by (fl32(S) desc, index asc): the number of larger keys, counted
+    // by `sub` threads per (token, expert) over E32 / sub keys each, 8 keys
+    // (four 16-byte LDS reads) at a time
+    {
+        int sub = 1;
+        while (sub < 4 && TG * E * sub * 2 <= RC_THREADS) sub *= 2;
+        const int span = E32 / sub;
+        for (int q = tid; q < TG * E * sub; q += RC_THREADS) {
+            const int pr = q / sub, part = q - pr * sub, tt = pr / E, e = pr - tt * E;
+            if (t0 + tt >= T) continue;
+            const unsigned long long my = key_s[tt][e];
+            int cnt = 0;
+            for (int c = part * span; c < (part + 1) * span; c += 8) {
+                const ulonglong2 *kp = (const ulonglong2 *)&key_s[tt][c];
+                ulonglong2 v[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = kp[i];
+#pragma unroll
+                for (int i = 0; i < 4; i++) cnt += (v[i].x > my ? 1 : 0) + (v[i].y > my ? 1 : 0);
+            }
+            atomicAdd(&rank_s[tt][e], cnt);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < PER; r++) {
+        const int p = tid + RC_THREADS * r, tt = p / E, e = p - tt * E;
+        if (tt >= TG || t0 + tt >= T) continue;
+        const int rank = rank_s[tt][e];
+        if (rank < k) {
+            ord_s[tt][rank] = e;
+            sel_s[tt][e] = 1;
+        } else {
+            atomicMax(&hi_s[tt], order_key_d(sS[tt][e] + (double)sB[tt][e]));
+        }
+    }
+    __syncthreads();
+    if (wave < TG && t0 + wave < T) {
+        const int tt = wave, t = t0 + tt;
+        const double bmax = (double)__uint_as_float(bmax_s[tt]);
+        const double ulp2 = 2.0 * f32_ulp(__builtin_bit_cast(double, smax_s[tt]));
+        const unsigned long long hk = hi_s[tt];
+        const double hi = hk == 0ull ? -INFINITY
+                                     : __builtin_bit_cast(double, (hk & 0x8000000000000000ull) ? (hk & ~0x8000000000000000ull)
+                                                                                               : ~hk);
+        const int e_top = ord_s[tt][0];
+        const double s_top = sS[tt][e_top], b_top = sB[tt][e_top];
+        bool ok = !bad_s[tt];
+        double tau_k = 0.0;
+        int my_e = 0;
+        if (lane < k) {
+            my_e = ord_s[tt][lane];
+            const double sa = sS[tt][my_e], ba = sB[tt][my_e];
+            double lo, sb;
+            if (lane + 1 < k) {
+                const int eb = ord_s[tt][lane + 1];
+                sb = sS[tt][eb];
+                lo = sb + (double)sB[tt][eb];
+            } else {
+                sb = hi;
+                lo = hi;
+            }
+            const double span = (sb > -INFINITY ? s_top - sb : 0.0) + b_top + bmax;
+            const double tau = 0x1.0p-18 + ulp2 + 0x1.0p-23 * span;
+            // strictly separated, and the reference's expf of l - max stays normal
+            ok = ok && sa - ba > lo + tau && s_top - sa < 64.0;
+            if (lane + 1 == k) tau_k = tau;
+        }
+        const bool certified = __all(ok);
+        if (lane == 0 && ca.stats != nullptr) atomicAdd(&ca.stats[certified ? 0 : 1], 1ull);
+        float l[ROUTE_EPL];
+#pragma unroll
+        for (int j = 0; j < ROUTE_EPL; j++) {
+            const int e = lane + WAVE * j;
+            l[j] = e < E ? (float)sS[tt][e] : -INFINITY;
+        }
+        if (certified) {
+            emit_ranked(a, t, l, lane < k ? (float)sS[tt][my_e] : 0.f, (float)s_top, my_e, lane);
+        } else {
+            // candidates: the top k, and every expert whose interval reaches
+            // the k-th's (all experts when some value is not finite)
+            tau_k = readlane_d(tau_k, k - 1);
+            const double thr = sS[tt][ord_s[tt][k - 1]] - bmax - ulp2 - tau_k - 0x1.0p-18;
+            const bool all = bad_s[tt] != 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int e = lane + WAVE * j;
+                const bool in = e < E && (all || sel_s[tt][e] || sS[tt][e] + (double)sB[tt][e] >= thr);
+                const uint64_t m = __ballot(in);
+                if (lane == 0) cand_s[tt][j] = m;
+            }
+            if (lane == 0) fail_s[tt] = 1;
+        }
+    }
+    __syncthreads();
+    bool any = false;
+    for (int tt = 0; tt < TG; tt++) {
+        if (!fail_s[tt]) continue;                          // uniform over the workgroup
+        any = true;
+        const uint64_t cand[4] = { cand_s[tt][0], cand_s[tt][1], cand_s[tt][2], cand_s[tt][3] };
+        cert_repair(x, K, w, wstride, t0 + tt, cand, (float *)a.logits + (int64_t)(t0 + tt) * a.logit_stride,
+                    ca.nb, rc_prod);
+    }
+    if (any) {
+        __threadfence();
+        __syncthreads();
+        if (wave < TG && fail_s[wave]) route_token(a, t0 + wave, wave, lane);
+    }
+}
+
+// bfac of the certified router for rows of K = 256 L values (see above):
+// B = bfac * A_computed bounds |reference logit - S|.  0 when K is too long
+// for the bound to stay tight.  The device's prefix of element i (lane-local
+// prefix of <= L terms, a 6-level wave scan of lane totals, <= 3 wave totals)
+// is within (3L + 14) u P + u |prefix| of the exact one, P = sum |p_i| <= 2 A;
+// its sum of |prefix| runs through <= L + 10 roundings, and so does the
+// fp64 S.
+static double router_cert_bfac(int K)
+{
+    const double u = 0x1.0p-24;
+    const double L = K / 256.0;
+    const double d_a = 1.0 - 2.01 * K * (3.0 * L + 14.0) * u;
+    if (d_a < 0.9 || K * u > 0.01) return 0.0;
+    const double a_fac = (1.0 + u) / (1.0 - (L + 10.0) * u) / d_a;
+    const double b = (u / (1.0 - K * u) + (L + 10.0) * 0x1.0p-52) * a_fac;
+    return b * (1.0 + 0x1.0p-8);                                     // fp32 product bfac * A
+}
+
+bool router_cert_ok(int K, int E, int k)
+{
+    return K % 256 == 0 && K >= 256 && K <= 4096 && E >= 1 && E <= ROUTE_MAX_E && k >= 1 && k <= E &&
+           k + 1 <= WAVE && router_cert_bfac(K) > 0.0;
+}
+
+size_t router_cert_scratch(int T, int E) { return (size_t)T * E * (sizeof(double) + sizeof(float)) + 256; }
+
+template <int L, int TG>
+static void cert_sums(const float *x, int T, int K, int E, const float *w, int64_t wstride, float *logits,
+                      int64_t ldl, _Float16 *x16, const CertArgs &ca, hipStream_t s)
+{
+    const dim3 grid((unsigned)((T + TG - 1) / TG), (unsigned)E);
+    hipLaunchKernelGGL((k_router_sums<L, TG>), grid, dim3(RC_THREADS), 0, s, x, T, K, E, w, wstride, logits, ldl, x16,
+                       ca);
+}
+
+template <int TG>
+static void cert_select(const float *x, int T, int K, const float *w, int64_t wstride, const CertArgs &ca,
+                        const RouteArgs &ra, hipStream_t s)
+{
+    const size_t lds = (size_t)ca.nb * (K + 4) * sizeof(float);
+    hipLaunchKernelGGL((k_router_select<TG>), dim3((unsigned)((T + TG - 1) / TG)), dim3(RC_THREADS), lds, s, x, K, w,
+                       wstride, ca, ra);
+}
+
+hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, const uint8_t *rw, uint64_t rstride,
+                              float *wf32, float *logits, int64_t ldl, _Float16 *x16, const RouteArgs &ra,
+                              void *scratch, unsigned long long *stats, hipStream_t s)
+{
+    if (T <= 0 || !router_cert_ok(K, E, ra.k) || !router_seq_type_ok(rtype, K) || ra.logits != logits ||
+        ra.logit_stride != ldl || ra.T != T || ra.E != E || ra.idx == nullptr)
+        return hipErrorInvalidValue;
+    if (((uintptr_t)x & 15) != 0 || ((uintptr_t)x16 & 15) != 0 || ((uintptr_t)scratch & 7) != 0)
+        return hipErrorInvalidValue;
+    const float *w = (const float *)rw;
+    int64_t wstride = (int64_t)(rstride / 4);
+    const bool f32_direct = rtype == T_F32 && rstride % 16 == 0 && ((uintptr_t)rw & 15) == 0;
+    if (!f32_direct) {
+        if (wf32 == nullptr || ((uintptr_t)wf32 & 15) != 0) return hipErrorInvalidValue;
+        const dim3 grid((unsigned)((K + 255) / 256), (unsigned)E);
+        switch (rtype) {
+        case T_F32: hipLaunchKernelGGL(k_router_rows_f32<T_F32>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
+        case T_F16: hipLaunchKernelGGL(k_router_rows_f32<T_F16>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
+        case T_Q8_0: hipLaunchKernelGGL(k_router_rows_f32<T_Q8_0>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
+        case T_Q4_K: hipLaunchKernelGGL(k_router_rows_f32<T_Q4_K>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
+        default: hipLaunchKernelGGL(k_router_rows_f32<T_Q6_K>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
+        }
+        w = wf32;
+        wstride = K;
+    }
+    const int TG = T == 1 ? 1 : T == 2 ? 2 : 4;
+    CertArgs ca;
+    ca.S = (double *)scratch;
+    ca.B = (float *)((uint8_t *)scratch + (((size_t)T * E * sizeof(double) + 255) & ~(size_t)255));
+    ca.bfac = (float)router_cert_bfac(K);
+    ca.stats = stats;
+    // repair batch: up to 13 candidate rows (about 104 KiB of LDS) while one
+    // token group is routed, up to 4 (~32 KiB) when several workgroups share CUs
+    const int rowb = (K + 4) * (int)sizeof(float);
+    ca.nb = T <= 4 ? min(13, 106496 / rowb) : min(4, 33792 / rowb);
+    if (ca.nb < 1) ca.nb = 1;
+#define DS3_CERT_SUMS(LV)                                                                        \
+    do {                                                                                         \
+        if (TG == 1) cert_sums<LV, 1>(x, T, K, E, w, wstride, logits, ldl, x16, ca, s);          \
+        else if (TG == 2) cert_sums<LV, 2>(x, T, K, E, w, wstride, logits, ldl, x16, ca, s);     \
+        else cert_sums<LV, 4>(x, T, K, E, w, wstride, logits, ldl, x16, ca, s);                  \
+    } while (0)
+    switch (K / 256) {
+    case 1: DS3_CERT_SUMS(1); break;
+    case 2: DS3_CERT_SUMS(2); break;
+    case 3: DS3_CERT_SUMS(3); break;
+    case 4: DS3_CERT_SUMS(4); break;
+    case 5: DS3_CERT_SUMS(5); break;
+    case 6: DS3_CERT_SUMS(6); break;
+    case 7: DS3_CERT_SUMS(7); break;
+    case 8: DS3_CERT_SUMS(8); break;
+    case 9: DS3_CERT_SUMS(9); break;
+    case 10: DS3_CERT_SUMS(10); break;
+    case 11: DS3_CERT_SUMS(11); break;
+    case 12: DS3_CERT_SUMS(12); break;
+    case 13: DS3_CERT_SUMS(13); break;
+    case 14: DS3_CERT_SUMS(14); break;
+    case 15: DS3_CERT_SUMS(15); break;
+    case 16: DS3_CERT_SUMS(16); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef DS3_CERT_SUMS
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (TG == 1) cert_select<1>(x, T, K, w, wstride, ca, ra, s);
+    else if (TG == 2) cert_select<2>(x, T, K, w, wstride, ca, ra, s);
+    else cert_select<4>(x, T, K, w, wstride, ca, ra, s);
+    return hipGetLastError();
+}
+
 bool router_seq_type_ok(int rtype, int K)
 {
     if (K <= 0) return false;

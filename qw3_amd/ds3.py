@@ -179,6 +179,21 @@ def set_prefill_min_tokens(n: int) -> int:
     return hip().ds3_hip_set_prefill_min_tokens(n)
 
 
+ROUTER_AUTO, ROUTER_SEQUENTIAL, ROUTER_CERTIFIED = 0, 1, 2
+
+
+def set_router_mode(mode: int) -> int:
+    """Router selection (ds3_hip_set_router_mode); returns the previous mode."""
+    return hip().ds3_hip_set_router_mode(mode)
+
+
+def router_stats(reset: bool = False) -> tuple[int, int]:
+    """(tokens certified, tokens repaired) by the certified router."""
+    c, r = C.c_uint64(), C.c_uint64()
+    _check(hip().ds3_hip_router_stats(C.byref(c), C.byref(r), 1 if reset else 0), "router_stats")
+    return c.value, r.value
+
+
 def device_info() -> dict:
     arch = C.create_string_buffer(64)
     ncu = C.c_int()

@@ -77,3 +77,28 @@ def index_mismatches(got_idx: np.ndarray, want_idx: np.ndarray, probs: np.ndarra
               f"{' (tie)' if tie else ''}", flush=True)
         unexplained += 0 if tie else 1
     return unexplained
+
+
+def cert_bfac(K: int) -> float:
+    """The certified router's bound factor for K-long logits: B = bfac * A
+    bounds |reference logit - S|, S the exact sum of the reference's fp32
+    products and A = sum_k |s_k| over their exact prefix sums.  The reference's
+    k-th partial sum rounds once, by at most u |s^_k| (u = 2^-24), so its
+    total error is at most u sum_k |s^_k| <= u A / (1 - K u); the remaining
+    factors cover the device's own fp32 evaluation of A and fp64 sum."""
+    u = 2.0 ** -24
+    L = K / 256
+    a_fac = (1 + u) / (1 - (L + 10) * u) / (1 - 2.01 * K * (3 * L + 14) * u)
+    return (u / (1 - K * u) + (L + 10) * 2.0 ** -52) * a_fac
+
+
+def cert_bound(x: np.ndarray, wr: np.ndarray) -> np.ndarray:
+    """[T][E]: bfac * sum_k |s_k| from exact (fp64) prefix sums of the fp32
+    products x[t][i] * wr[e][i]."""
+    T, K = x.shape
+    bfac = cert_bfac(K)
+    out = np.empty((T, wr.shape[0]))
+    for t in range(T):
+        pr = (x[t][None, :] * wr).astype(np.float32).astype(np.float64)
+        out[t] = bfac * np.abs(np.cumsum(pr, axis=1)).sum(axis=1)
+    return out

@@ -4,11 +4,13 @@ same seeded inputs.
 Bars: top-k expert indices identical to the oracle's (its sequential-sum
 logits) barring exact ties; combined outputs within max-abs 2e-3 and rel-L2
 1e-3 of the FP32 oracle; bucketing identical."""
+from contextlib import contextmanager
+
 import numpy as np
 import pytest
 
 import _oracle as O
-from _cases import Case, assert_close, index_mismatches
+from _cases import Case, assert_close, cert_bound, index_mismatches
 from qw3_amd import ds3
 from qw3_amd import workload as W
 
@@ -71,41 +73,88 @@ def logit_bits_differ(got: np.ndarray, want: np.ndarray) -> int:
     return int((~same).sum())
 
 
+MODES = [ds3.ROUTER_SEQUENTIAL, ds3.ROUTER_CERTIFIED]
+
+
+@contextmanager
+def router_mode(mode: int):
+    prev = ds3.set_router_mode(mode)
+    try:
+        yield
+    finally:
+        ds3.set_router_mode(prev)
+
+
+def cert_applies(K: int, E: int) -> bool:
+    """Shapes the certified router serves (K a multiple of 256 up to 4096, E <= 256)."""
+    return K % 256 == 0 and 256 <= K <= 4096 and E <= 256
+
+
+def check_logits(gl: np.ndarray, ol: np.ndarray, x: np.ndarray, wr: np.ndarray, mode: int):
+    """Sequential router: the reference's logits bit for bit.  Certified
+    router: every logit within the proven bound of the reference's (plus its
+    own fp32 rounding).  Returns the bound (None for bit-exact)."""
+    if mode == ds3.ROUTER_SEQUENTIAL or not cert_applies(x.shape[1], wr.shape[0]):
+        assert logit_bits_differ(gl, ol) == 0       # the reference's sequential fp32 sums, bit for bit
+        return None
+    B = cert_bound(x, wr)
+    err = np.abs(gl.astype(np.float64) - ol.astype(np.float64))
+    assert (err <= B + np.spacing(np.abs(gl)).astype(np.float64)).all()
+    exact = gl.view(np.uint32) == ol.view(np.uint32)
+    print(f"    certified logits: max |err|/bound {float(np.max(err / np.maximum(B, 1e-30))):.3f}, "
+          f"{exact.mean():.1%} bit-equal", flush=True)
+    return B
+
+
 # ---------------------------------------------------------------------------
 # routing
 # ---------------------------------------------------------------------------
 
+@pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("cfg,T", [("real", 64), ("uniform", 512), ("zipf", 2048), ("q80", 256)])
-def test_route_indices_bit_exact(hip_ready, request, cfg, T):
+def test_route_indices_bit_exact(hip_ready, request, cfg, T, mode):
     case = request.getfixturevalue(cfg)
     x = W.make_inputs({"real": 1, "uniform": 2, "zipf": 3, "q80": 5}[cfg], T, seed=77)
-    print(f"  route {cfg} T={T}", flush=True)
-    gi, gs, gl = gpu_route(case, x)
+    print(f"  route {cfg} T={T} mode={mode}", flush=True)
+    with router_mode(mode):
+        gi, gs, gl = gpu_route(case, x)
     oi, osc, probs, ol = oracle_route(case.wr, x, with_logits=True)
-    assert logit_bits_differ(gl, ol) == 0       # the reference's sequential fp32 sums, bit for bit
+    B = check_logits(gl, ol, x, case.wr, mode)
     assert index_mismatches(gi, oi, probs) == 0
     assert (gi == oi).all()
     rel = np.abs(gs - osc) / np.abs(osc)
     print(f"    weights: max rel diff {rel.max():.2e}", flush=True)
-    # same logits: the weights differ only by the device expf / division roundings
-    assert rel.max() < 2e-6
+    if B is None:
+        # same logits: the weights differ only by the device expf / division roundings
+        assert rel.max() < 2e-6
+    else:
+        # each log-weight moves by at most twice the largest logit bound of its token
+        assert (rel <= 2.2 * B.max(axis=1, keepdims=True) + 4e-6).all()
 
 
-def test_route_near_ties(hip_ready):
+@pytest.mark.parametrize("mode", MODES)
+def test_route_near_ties(hip_ready, mode):
     """Router rows 3 and 5 are row 0 shifted by ~1e-8 per element, so their
     logits sit ~5e-7 from row 0's: wider than a probability ulp, inside the
     rounding noise of a reordered fp32 sum.  Only the reference's own
-    summation order picks what the reference picks."""
+    summation order picks what the reference picks: the certified router
+    cannot certify these tokens and must repair them with the exact chains."""
     rng = np.random.default_rng(5)
     wr = (rng.standard_normal((16, 2048)) * 0.02).astype(np.float32)
     x = rng.standard_normal((64, 2048)).astype(np.float32)
     wr[3] = wr[0] + np.float32(1e-8)
     wr[5] = wr[0] - np.float32(1.5e-8)
-    gi, _, gl = route_raw(ds3.Buffer.from_array(wr), ds3.TYPE_F32, x, 16, 4)
+    with router_mode(mode):
+        gi, _, gl = route_raw(ds3.Buffer.from_array(wr), ds3.TYPE_F32, x, 16, 4)
     oi, _, probs, ol = oracle_route(wr, x, 4, with_logits=True)
-    assert logit_bits_differ(gl, ol) == 0
+    check_logits(gl, ol, x, wr, mode)
     assert index_mismatches(gi, oi, probs) == 0
     assert (gi == oi).all()
+    if mode == ds3.ROUTER_CERTIFIED:
+        # tokens that select expert 0 were repaired: the tied rows carry the exact chains
+        sel0 = (oi == 0).any(axis=1)
+        assert sel0.sum() > 0
+        assert logit_bits_differ(gl[sel0][:, [0, 3, 5]], ol[sel0][:, [0, 3, 5]]) == 0
 
 
 def _near_tie_router(type_: int, E: int, K: int, rng):
@@ -150,9 +199,10 @@ def _near_tie_router(type_: int, E: int, K: int, rng):
     return raw, wr, j
 
 
+@pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("type_,E", [(ds3.TYPE_F32, 24), (ds3.TYPE_F16, 16), (ds3.TYPE_Q8_0, 16),
                                      (ds3.TYPE_Q8_0, 24), (ds3.TYPE_Q4_K, 16), (ds3.TYPE_Q6_K, 16)])
-def test_route_router_types(hip_ready, type_, E):
+def test_route_router_types(hip_ready, type_, E, mode):
     """Near ties on every router type, E not a multiple of the 64 experts of
     a wave included: the router rows are expanded to the values of the
     reference's FP32 copy and summed in its order, so logits are bit-exact
@@ -163,10 +213,11 @@ def test_route_router_types(hip_ready, type_, E):
     x = rng.standard_normal((T, K)).astype(np.float32)
     if j is not None:
         x[:, j] = np.float32(1e-3)            # one code step of that weight moves the logit ~1e-7
-    gi, _, gl = route_raw(ds3.Buffer.from_array(raw), type_, x, E, k)
+    with router_mode(mode):
+        gi, _, gl = route_raw(ds3.Buffer.from_array(raw), type_, x, E, k)
     oi, _, probs, ol = oracle_route(wr, x, k, with_logits=True)
-    print(f"    {ds3.TYPE_NAMES[type_]} E={E}", flush=True)
-    assert logit_bits_differ(gl, ol) == 0
+    print(f"    {ds3.TYPE_NAMES[type_]} E={E} mode={mode}", flush=True)
+    check_logits(gl, ol, x, wr, mode)
     assert index_mismatches(gi, oi, probs) == 0
     assert (gi == oi).all()
 
@@ -185,10 +236,12 @@ def test_moe_ffn_router_logits(hip_ready, type_):
     assert logit_bits_differ(lb.read(np.float32, (E,)), O.vec_matmul(x, wr)) == 0
 
 
-@pytest.mark.parametrize("T,K,E,align", [(1, 2048, 128, 0), (5, 2048, 128, 0), (17, 2048, 128, 0),
-                                         (32, 1000, 72, 0), (37, 1000, 72, 0), (130, 2048, 128, 4),
-                                         (1100, 512, 128, 0)])
-def test_route_logits_shapes(hip_ready, T, K, E, align):
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("T,K,E,align", [(1, 2048, 128, 0), (2, 2048, 128, 0), (5, 2048, 128, 0),
+                                         (17, 2048, 128, 0), (32, 1000, 72, 0), (37, 1000, 72, 0),
+                                         (130, 2048, 128, 4), (1100, 512, 128, 0), (6, 1536, 200, 0),
+                                         (3, 4096, 256, 0)])
+def test_route_logits_shapes(hip_ready, T, K, E, align, mode):
     """Both router kernels (products split off for T <= 32, one lane per
     chain above): ragged T (workgroup tails), K not a multiple of the chunk
     width (scalar tail), E not a multiple of 16, an x row start that is only
@@ -204,10 +257,12 @@ def test_route_logits_shapes(hip_ready, T, K, E, align):
     else:
         xb = ds3.Buffer.from_array(x)
     ib, sb, lb = ds3.Buffer.alloc(T * k * 4), ds3.Buffer.alloc(T * k * 4), ds3.Buffer.alloc(T * E * 4)
-    ds3.moe_route(xb, ds3.Buffer.from_array(wr), ds3.TYPE_F32, T, K, E, k, ib, sb, lb)
+    with router_mode(mode):
+        ds3.moe_route(xb, ds3.Buffer.from_array(wr), ds3.TYPE_F32, T, K, E, k, ib, sb, lb)
     gl = lb.read(np.float32, (T, E))
     oi, _, probs, ol = oracle_route(wr, x, k, with_logits=True)
-    assert logit_bits_differ(gl, ol) == 0
+    # a 4-byte aligned x row start keeps the sequential router (16-byte loads)
+    check_logits(gl, ol, x, wr, ds3.ROUTER_SEQUENTIAL if align else mode)
     assert (ib.read(np.int32, (T, k)) == oi).all()
 
 
@@ -266,7 +321,7 @@ def test_decode_T1_config1(hip_ready, real):
         assert np.array_equal(gi[0], oi[t])
         got[t] = o[0]
     err, rl = assert_close(got, want)
-    assert rl < 1e-5           # the fp32 GEMV path is far inside the bar
+    assert rl < 5e-5           # the fp32 GEMV path is far inside the bar
 
 
 def test_prefill_T512_config2(hip_ready, uniform):
@@ -307,7 +362,7 @@ def test_decode_and_prefill_paths_agree(hip_ready, real):
     a, ai, _, _ = real.gpu_batch(x, prefill_min=1 << 30)     # GEMV path
     b, bi, _, _ = real.gpu_batch(x, prefill_min=1)           # grouped MFMA path
     assert np.array_equal(ai, oi) and np.array_equal(bi, oi)
-    assert_close(a, want, rel_l2=1e-5)
+    assert_close(a, want, rel_l2=5e-5)
     assert_close(b, want)
 
 
