@@ -76,6 +76,10 @@ def kernel_bytes(name, spec, T, counts, n_used):
         "moe_decode_gate_up": distinct * gu + T * K * 4 + S * F * 4,
         "moe_decode_down": distinct * dn + S * F * 4 + T * K * 4,
         "router_logits": W.router_bytes(spec) + T * K * 4 + T * E * 4,
+        # certified router: the sums read the router and x, write S, B and the logits;
+        # the selection reads S and B
+        "router_sums": W.router_bytes(spec) + T * K * 4 + T * E * (8 + 4 + 4),
+        "router_select": T * E * (8 + 4),
     }.get(name)
 
 

@@ -657,9 +657,14 @@ int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstrid
     hipError_t e;
     if (use_cert(x, T, n_embd, n_expert, n_used, allow_cert)) {
         {
-            KScope ks("router_logits");
+            KScope ks("router_sums");
             e = launch_router_cert(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, rb.wf32,
-                                   rb.logits, n_expert, rb.x16, ra, rb.cert, g.cert_stats, g.stream);
+                                   rb.logits, n_expert, rb.x16, ra, rb.cert, g.cert_stats, 1, g.stream);
+        }
+        if (e == hipSuccess) {
+            KScope ks("router_select");
+            e = launch_router_cert(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, rb.wf32,
+                                   rb.logits, n_expert, rb.x16, ra, rb.cert, g.cert_stats, 2, g.stream);
         }
         if (x16_done) *x16_done = rb.x16 != nullptr;
         return report(e, "router (certified)");

@@ -65,11 +65,13 @@ hipError_t launch_router_seq(const float *x, int T, int K, int E, int rtype, con
 // repaired candidates).  ra must describe these logits; scratch:
 // router_cert_scratch(T, E) bytes, 8-byte aligned; x, x16 16-byte aligned.
 // stats (optional): device counters {tokens certified, tokens repaired}.
+// phases: bit 0 enqueues the sums (after the FP32 row copy of a non-F32
+// router), bit 1 the selection; the same arguments go to both.
 bool router_cert_ok(int K, int E, int k);
 size_t router_cert_scratch(int T, int E);
 hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, const uint8_t *rw, uint64_t rstride,
                               float *wf32, float *logits, int64_t ldl, _Float16 *x16, const RouteArgs &ra,
-                              void *scratch, unsigned long long *stats, hipStream_t s);
+                              void *scratch, unsigned long long *stats, int phases, hipStream_t s);
 
 // Decode (small T) expert products.
 //   h[slot][F] = silu(x[t] . Wg_e) * (x[t] . Wu_e), slot = t*n_used + k, e = idx[slot]

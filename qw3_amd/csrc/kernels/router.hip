@@ -1152,7 +1152,7 @@ static void cert_select(const float *x, int T, int K, const float *w, int64_t ws
 
 hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, const uint8_t *rw, uint64_t rstride,
                               float *wf32, float *logits, int64_t ldl, _Float16 *x16, const RouteArgs &ra,
-                              void *scratch, unsigned long long *stats, hipStream_t s)
+                              void *scratch, unsigned long long *stats, int phases, hipStream_t s)
 {
     if (T <= 0 || !router_cert_ok(K, E, ra.k) || !router_seq_type_ok(rtype, K) || ra.logits != logits ||
         ra.logit_stride != ldl || ra.T != T || ra.E != E || ra.idx == nullptr)
@@ -1164,6 +1164,8 @@ hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, co
     const bool f32_direct = rtype == T_F32 && rstride % 16 == 0 && ((uintptr_t)rw & 15) == 0;
     if (!f32_direct) {
         if (wf32 == nullptr || ((uintptr_t)wf32 & 15) != 0) return hipErrorInvalidValue;
+    }
+    if (!f32_direct && (phases & 1)) {
         const dim3 grid((unsigned)((K + 255) / 256), (unsigned)E);
         switch (rtype) {
         case T_F32: hipLaunchKernelGGL(k_router_rows_f32<T_F32>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
@@ -1172,6 +1174,8 @@ hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, co
         case T_Q4_K: hipLaunchKernelGGL(k_router_rows_f32<T_Q4_K>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
         default: hipLaunchKernelGGL(k_router_rows_f32<T_Q6_K>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
         }
+    }
+    if (!f32_direct) {
         w = wf32;
         wstride = K;
     }
@@ -1192,7 +1196,7 @@ hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, co
         else if (TG == 2) cert_sums<LV, 2>(x, T, K, E, w, wstride, logits, ldl, x16, ca, s);     \
         else cert_sums<LV, 4>(x, T, K, E, w, wstride, logits, ldl, x16, ca, s);                  \
     } while (0)
-    switch (K / 256) {
+    if (phases & 1) switch (K / 256) {
     case 1: DS3_CERT_SUMS(1); break;
     case 2: DS3_CERT_SUMS(2); break;
     case 3: DS3_CERT_SUMS(3); break;
@@ -1213,7 +1217,7 @@ hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, co
     }
 #undef DS3_CERT_SUMS
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess || !(phases & 2)) return e;
     if (TG == 1) cert_select<1>(x, T, K, w, wstride, ca, ra, s);
     else if (TG == 2) cert_select<2>(x, T, K, w, wstride, ca, ra, s);
     else cert_select<4>(x, T, K, w, wstride, ca, ra, s);
