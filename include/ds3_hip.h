@@ -199,7 +199,7 @@ void ds3_hip_profile_print(const char *label);
  *   zeroes); residual (optional) [T][n_embd] is added to output;
  *   indices / scores (optional) receive the routing [T][n_used];
  *   gate_logits (optional) receives the logits [T][n_expert].
- * Up to 64 tokens (see ds3_hip_set_router_mode) the router is the certified
+ * Up to 16 tokens (see ds3_hip_set_router_mode) the router is the certified
  * one: indices equal the reference's; gate_logits hold the fp32 rounding of
  * the exact sum of the reference's fp32 products (the reference's own
  * sequential sums for experts whose order needed them), within a proven
@@ -236,7 +236,7 @@ int ds3_hip_dequantize(const ds3_hip_buffer_t *src, uint64_t src_offset, ds3_hip
 
 /* Router selection.  0 (default): the certified router (fp64 wavefront sums
  * with a proven error bound, exact sequential sums only where the bound
- * cannot certify the top-k order) in ds3_hip_moe_ffn and, up to 64 tokens,
+ * cannot certify the top-k order) in ds3_hip_moe_ffn and, up to 16 tokens,
  * in ds3_hip_moe_ffn_batch; the reference's sequential-order sums (logits
  * bit-identical to the reference's) everywhere else.  1: sequential-order
  * sums everywhere.  2: the certified router wherever its shape limits allow

@@ -30,7 +30,7 @@ namespace {
 
 constexpr int kDefaultPrefillMin = 16;
 constexpr int kTickets = 32;             // router token-group tickets (zero between launches)
-constexpr int kCertMaxTokens = 64;       // automatic mode: certified router up to this many tokens
+constexpr int kCertMaxTokens = 16;       // automatic mode: certified router up to this many tokens
 constexpr size_t kAllocPad = 256;        // slack after every allocation: kernels read whole dwords
 
 struct KRec {

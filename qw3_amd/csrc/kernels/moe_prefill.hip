@@ -499,12 +499,15 @@ bool grouped_type_ok(int type, int K)
     return type == T_Q4_K || type == T_Q6_K || type == T_Q8_0;
 }
 
-// n tiles per run (tuning knobs).
+// n tiles per run (tuning knobs): at T = 512 (about 128 work items) these
+// give each persistent workgroup one long run (gate_up: 2 runs of 3 n tiles
+// per item; down: 2 runs of 8), so the stream's start-up latency is paid
+// once per workgroup.
 #ifndef DS3_GU_NTB
-#define DS3_GU_NTB 1
+#define DS3_GU_NTB 3
 #endif
 #ifndef DS3_DN_NTB
-#define DS3_DN_NTB 4
+#define DS3_DN_NTB 8
 #endif
 
 // Persistent grid: one workgroup per CU (a multiple of 8), walking
