@@ -10,7 +10,8 @@ the 256 MB Infinity Cache between steps.  The line also carries the T = 1
 decode figures (configs[0] shape) under "t1".
 
 roofline: the dominant kernel's algorithmic bytes per launch / its mean
-duration, timed with HIP events on the library stream inside the timed region.
+duration, timed with HIP events on the library stream over a second pass of
+the same K steps (the timed region itself carries no per-kernel events).
 cpu_baseline: the reference's own ds3_ref_moe_ffn (compiled from its sources
 into oracle/_ref) on the host cores, FP32-dequantised weights resident, on a
 bounded sample of the same workload.
@@ -74,6 +75,8 @@ def kernel_bytes(name, spec, T, counts, n_used):
         "moe_grouped_gate_up": distinct * gu + T * K * 2 + S * F * 2,
         "moe_grouped_down": distinct * dn + S * F * 2 + S * K * 4,
         "moe_decode_gate_up": distinct * gu + T * K * 4 + S * F * 4,
+        # with the certified selection in its prologue: also reads S and B
+        "moe_decode_gate_up_sel": distinct * gu + T * K * 4 + S * F * 4 + T * E * (8 + 4),
         "moe_decode_down": distinct * dn + S * F * 4 + T * K * 4,
         "router_logits": W.router_bytes(spec) + T * K * 4 + T * E * 4,
         # certified router: the sums read the router and x, write S, B and the logits;
@@ -85,8 +88,8 @@ def kernel_bytes(name, spec, T, counts, n_used):
 
 def run_gpu(args, T, steps, warmup, layers, xs, spec, n_used=8):
     """Warmup steps with every kernel timed (per-kernel breakdown, choice of
-    the dominant kernel), then the timed steps with only the dominant kernel
-    bracketed by events, so the other launches run back to back."""
+    the dominant kernel), the timed steps with no per-kernel events, then the
+    same steps again with only the dominant kernel bracketed by events."""
     from qw3_amd import ds3
     from qw3_amd._native import hip
     E, K = spec.n_expert, spec.n_embd
@@ -113,10 +116,8 @@ def run_gpu(args, T, steps, warmup, layers, xs, spec, n_used=8):
     breakdown = ds3.kernel_stats()
     dominant = max((k for k in breakdown if kernel_bytes(k, spec, T, counts, n_used) is not None),
                    key=lambda k: breakdown[k][1])
-    # timed region: synchronise, K steps enqueued back to back, synchronise
-    hip().ds3_hip_kernel_timing_reset()
-    hip().ds3_hip_kernel_timing_only(dominant.encode())
-    hip().ds3_hip_kernel_timing(1)
+    # timed region: synchronise, K steps enqueued back to back, synchronise;
+    # no per-kernel events in it (at T = 1 an event pair costs a third of a step)
     hip().ds3_hip_synchronize()
     hip().ds3_hip_begin_batch()
     t0 = time.perf_counter()
@@ -126,6 +127,15 @@ def run_gpu(args, T, steps, warmup, layers, xs, spec, n_used=8):
     gpu_ms = hip().ds3_hip_timer_stop_ms()
     hip().ds3_hip_end_batch()
     wall_ms = (time.perf_counter() - t0) * 1e3
+    # the same K steps again with only the dominant kernel bracketed by
+    # events on the library's stream: its average duration for the roofline
+    hip().ds3_hip_kernel_timing_reset()
+    hip().ds3_hip_kernel_timing_only(dominant.encode())
+    hip().ds3_hip_kernel_timing(1)
+    hip().ds3_hip_begin_batch()
+    for i in range(steps):
+        step(i)
+    hip().ds3_hip_end_batch()
     hip().ds3_hip_kernel_timing(0)
     hip().ds3_hip_kernel_timing_only(None)
     stats = ds3.kernel_stats()

@@ -8,6 +8,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -31,6 +32,13 @@ namespace {
 constexpr int kDefaultPrefillMin = 16;
 constexpr int kTickets = 32;             // router token-group tickets (zero between launches)
 constexpr int kCertMaxTokens = 16;       // automatic mode: certified router up to this many tokens
+#ifndef DS3_FUSE_SELECT_MAX_T
+#define DS3_FUSE_SELECT_MAX_T 1          // decode: certified selection inside the gate/up kernel up to this T
+#endif
+constexpr int kFuseSelMaxTokens = DS3_FUSE_SELECT_MAX_T;
+#ifndef DS3_FUSED_NB
+#define DS3_FUSED_NB 4                   // repair batch rows of the fused selection at T <= 2
+#endif
 constexpr size_t kAllocPad = 256;        // slack after every allocation: kernels read whole dwords
 
 struct KRec {
@@ -189,15 +197,28 @@ bool fits(const ds3_hip_buffer_t *b, size_t need, const char *what)
     return true;
 }
 
+// A certified selection left to the decode gate/up kernel's prologue
+// (launch_decode_gate_up_sel): set by route_tokens when the caller allows it.
+struct DeferredSel {
+    bool on = false;
+    CertSel cs{};
+    RouteArgs ra{};
+};
+
 // Per-token expert products for `slots` routed slots of T tokens:
 // h = swiglu(gate, up) then out (+)= sum_k w_k * down(h_k).
 int run_experts_decode(const float *x, int64_t ldx, const int32_t *idx, const float *wts, int T, int n_used,
                        const ExpertWeights &ew, uint32_t n_embd, uint32_t n_ff, float *out, const float *residual,
-                       bool accumulate, float *h, float *tmp_up)
+                       bool accumulate, float *h, float *tmp_up, const DeferredSel *sel = nullptr)
 {
     const int slots = T * n_used;
     hipError_t e;
-    if (ew.gate_type == ew.up_type) {
+    if (sel != nullptr && sel->on) {
+        // route_tokens defers only where this kernel applies (same gate/up
+        // types, rows n_embd floats apart)
+        KScope ks("moe_decode_gate_up_sel");
+        e = launch_decode_gate_up_sel(x, T, n_used, ew, (int)n_embd, (int)n_ff, h, sel->cs, sel->ra, g.stream);
+    } else if (ew.gate_type == ew.up_type) {
         KScope ks("moe_decode_gate_up");
         e = launch_decode_gate_up(x, ldx, idx, slots, n_used, ew, (int)n_embd, (int)n_ff, h, g.stream);
     } else {
@@ -639,10 +660,12 @@ bool use_cert(const float *x, int T, uint32_t n_embd, uint32_t n_expert, uint32_
 }
 
 // Router logits + softmax/top-k/renorm for T tokens.  Sets *x16_done when the
-// router also wrote rb.x16.
+// router also wrote rb.x16.  With defer, a certified selection may be left to
+// the decode gate/up kernel (defer->on): the routing outputs are then written
+// by that kernel.
 int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstride, int rtype, int T, uint32_t n_embd,
                  uint32_t n_expert, uint32_t n_used, bool norm, const RouteBufs &rb, bool *x16_done = nullptr,
-                 bool allow_cert = false)
+                 bool allow_cert = false, DeferredSel *defer = nullptr)
 {
     RouteArgs ra{};
     ra.logits = rb.logits;
@@ -661,7 +684,18 @@ int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstrid
             e = launch_router_cert(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, rb.wf32,
                                    rb.logits, n_expert, rb.x16, ra, rb.cert, g.cert_stats, 1, g.stream);
         }
-        if (e == hipSuccess) {
+        if (e == hipSuccess && defer != nullptr && T <= kFuseSelMaxTokens) {
+            // repair batch of the fused kernel: 4 candidate rows (~32 KiB of
+            // LDS at K = 2048) keep 3 of its workgroups per CU at T <= 2
+            const int rowb = ((int)n_embd + 4) * 4;
+            const int nb = std::max(1, std::min(T <= 2 ? DS3_FUSED_NB : 2, 33792 / rowb));
+            e = router_cert_sel(T, (int)n_embd, (int)n_expert, (int)n_used, rtype, cptr(router), rstride, rb.wf32,
+                                rb.cert, g.cert_stats, nb, &defer->cs);
+            if (e == hipSuccess) {
+                defer->on = true;
+                defer->ra = ra;
+            }
+        } else if (e == hipSuccess) {
             KScope ks("router_select");
             e = launch_router_cert(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, rb.wf32,
                                    rb.logits, n_expert, rb.x16, ra, rb.cert, g.cert_stats, 2, g.stream);
@@ -746,8 +780,9 @@ extern "C" int ds3_hip_moe_ffn(
     float *sc = (float *)(ws + o_sc), *h = (float *)(ws + o_h), *tmp = (float *)(ws + o_t);
     const float *x = fptr(input);
     const RouteBufs rb = route_bufs(ws + o_r, rs, fptr(gate_logits), idx, sc, nullptr);
+    DeferredSel sel;
     if (route_tokens(x, w_gate_inp, router_row_stride, router_type, 1, n_embd, n_expert, n_used, norm_topk_prob,
-                     rb, nullptr, true) != 0)
+                     rb, nullptr, true, gate_type == up_type ? &sel : nullptr) != 0)
         return -1;
     if (has_shared &&
         run_shared(x, w_shared_gate, w_shared_up, w_shared_down, shared_gate_type, shared_up_type, shared_down_type,
@@ -757,7 +792,7 @@ extern "C" int ds3_hip_moe_ffn(
     ExpertWeights ew = make_ew(w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type, down_type, gate_row_stride,
                                up_row_stride, down_row_stride, expert_offsets);
     if (run_experts_decode(x, n_embd, idx, sc, 1, (int)n_used, ew, n_embd, n_ff_exp, fptr(output), nullptr, true, h,
-                           tmp) != 0)
+                           tmp, &sel) != 0)
         return -1;
     return finish(hipSuccess, "moe_ffn");
 }
@@ -1005,8 +1040,9 @@ extern "C" int ds3_hip_moe_ffn_batch(
                                     use_grouped ? (_Float16 *)(ws + o_x16) : nullptr);
     const float *x = fptr(input);
     bool x16_done = false;
+    DeferredSel sel;
     if (route_tokens(x, w_gate_inp, router_row_stride, router_type, (int)T, n_embd, n_expert, n_used, norm_topk_prob,
-                     rb, &x16_done, true) != 0)
+                     rb, &x16_done, true, !use_grouped && gate_type == up_type ? &sel : nullptr) != 0)
         return -1;
     ExpertWeights ew = make_ew(w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type, down_type, gate_row_stride,
                                up_row_stride, down_row_stride, expert_offsets);
@@ -1014,7 +1050,7 @@ extern "C" int ds3_hip_moe_ffn_batch(
     const float *res = residual ? fptr(residual) : nullptr;
     if (!use_grouped) {
         if (run_experts_decode(x, n_embd, rb.idx, rb.scores, (int)T, (int)n_used, ew, n_embd, n_ff_exp, out, res, true,
-                               (float *)(ws + o_h), (float *)(ws + o_t)) != 0)
+                               (float *)(ws + o_h), (float *)(ws + o_t), &sel) != 0)
             return -1;
         return finish(hipSuccess, "moe_ffn_batch");
     }

@@ -73,11 +73,37 @@ hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, co
                               float *wf32, float *logits, int64_t ldl, _Float16 *x16, const RouteArgs &ra,
                               void *scratch, unsigned long long *stats, int phases, hipStream_t s);
 
+// What the certified router's selection reads, for a kernel that selects in
+// its own prologue (launch_decode_gate_up_sel) after launch_router_cert's
+// phase 1 with the same arguments: the sums S and bounds B in scratch, the
+// bound factor, the repair batch (nb rows of K + 4 floats) and the FP32
+// router rows the sums were taken over.
+struct CertArgs {
+    double *S;                   // [T][E]
+    float *B;                    // [T][E]
+    float bfac;
+    int nb;                      // candidate rows per repair batch (dynamic LDS rows of K + 4 floats)
+    unsigned long long *stats;   // optional [2]: tokens certified, tokens repaired
+};
+struct CertSel {
+    CertArgs ca;
+    const float *w;              // FP32 router rows, wstride floats apart
+    int64_t wstride;
+};
+hipError_t router_cert_sel(int T, int K, int E, int k, int rtype, const uint8_t *rw, uint64_t rstride, float *wf32,
+                           void *scratch, unsigned long long *stats, int nb, CertSel *out);
+
 // Decode (small T) expert products.
 //   h[slot][F] = silu(x[t] . Wg_e) * (x[t] . Wu_e), slot = t*n_used + k, e = idx[slot]
 hipError_t launch_decode_gate_up(const float *x, int64_t ldx, const int32_t *idx, int n_slots,
                                  int n_used, const ExpertWeights &ew, int K, int F,
                                  float *h, hipStream_t s);
+// The same for the T tokens of x (rows K floats apart), with the expert of
+// each slot chosen in the kernel by the certified router's selection over
+// cs (launch_router_cert phase 1 done); writes ra.idx / ra.scores (and
+// repaired logits) as the selection launch would.
+hipError_t launch_decode_gate_up_sel(const float *x, int T, int n_used, const ExpertWeights &ew, int K, int F,
+                                     float *h, const CertSel &cs, const RouteArgs &ra, hipStream_t s);
 //   out[slot][F] = x[t] . W_e with W = ew.gate / gate_type / gate_stride and
 //   expert offsets from table column `which` (0 gate, 1 up).
 hipError_t launch_decode_proj(const float *x, int64_t ldx, const int32_t *idx, int n_slots, int n_used,

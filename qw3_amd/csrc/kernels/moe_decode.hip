@@ -7,8 +7,7 @@
 //   down:    out[t][j] = out[t][j] + w_0 y_0[j] + ... + w_{k-1} y_{k-1}[j]
 //            with y_k[j] = h[slot_k] . Wd_{e_k}[j], summed in top-k order
 //            (reference src/ds3_reference.c:674-678), no atomics.
-#include "common.h"
-#include "launch.h"
+#include "route_select.h"
 
 namespace ds3k {
 
@@ -25,19 +24,15 @@ constexpr int DEC_TPB = 256;
 // Lane group (G lanes) per row, UPL = K/32/G units per lane, RPW rows per
 // group: the trip counts are compile-time and rows past F are clamped (their
 // results dropped), so every load of a wave is issued before its first dot
-// product and the wave pays one memory round trip.
+// product and the wave pays one memory round trip.  Rows of expert e for
+// routed slot `slot` (token row xt).
 template <int GT, int G, int UPL, bool PAIR>
-__global__ void __launch_bounds__(DEC_TPB)
-k_decode_gate_up(const float *__restrict__ x, int64_t ldx, const int32_t *__restrict__ idx, int n_used,
-                 ExpertWeights ew, int K, int F, int which, float *__restrict__ h)
+__device__ __forceinline__ void gate_up_rows(const float *__restrict__ xt, int slot, int e, const ExpertWeights &ew,
+                                             int K, int F, int which, float *__restrict__ h)
 {
     constexpr int GPW = WAVE / G, RPW = 2;
-    const int slot = blockIdx.y;
-    const int t = slot / n_used;
-    const int e = idx[slot];
     const uint8_t *wg = expert_base(ew.gate, ew.table, e, PAIR ? 0 : which, (uint64_t)F, ew.gate_stride);
     const uint8_t *wu = PAIR ? expert_base(ew.up, ew.table, e, 1, (uint64_t)F, ew.up_stride) : wg;
-    const float *xt = x + (int64_t)t * ldx;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     const int gl = lane % G, grp = lane / G;
     const int r0 = (blockIdx.x * (DEC_TPB / WAVE) + wave) * GPW * RPW + grp;
@@ -67,6 +62,42 @@ k_decode_gate_up(const float *__restrict__ x, int64_t ldx, const int32_t *__rest
         const float b = PAIR ? group_sum<G>(au[i]) : 0.f;
         if (r < F && gl == 0) h[(int64_t)slot * F + r] = PAIR ? swiglu(a, b) : a;
     }
+}
+
+template <int GT, int G, int UPL, bool PAIR>
+__global__ void __launch_bounds__(DEC_TPB)
+k_decode_gate_up(const float *__restrict__ x, int64_t ldx, const int32_t *__restrict__ idx, int n_used,
+                 ExpertWeights ew, int K, int F, int which, float *__restrict__ h)
+{
+    const int slot = blockIdx.y;
+    gate_up_rows<GT, G, UPL, PAIR>(x + (int64_t)(slot / n_used) * ldx, slot, idx[slot], ew, K, F, which, h);
+}
+
+// gate_up with the certified router's selection in its prologue: every
+// wave ranks the experts of its token from the sums S / bounds B on its own
+// (no LDS, no barrier on the common path) and takes the expert of its slot;
+// a token it cannot certify is repaired by the whole workgroup.  Wave 0 of
+// workgroup x = 0 of each token's first slot also writes the token's
+// indices, weights (and repaired logits) for the down kernel and the caller,
+// after its products (a certified token's weights are not on their path).
+// This removes the selection launch and its memory round trip from the
+// decode chain.
+template <int GT, int G, int UPL>
+__global__ void __launch_bounds__(DEC_TPB)
+k_decode_gate_up_sel(const float *__restrict__ x, int n_used, ExpertWeights ew, int K, int F,
+                     float *__restrict__ h, CertSel cs, RouteArgs ra)
+{
+    extern __shared__ __attribute__((aligned(16))) float sel_prod[];
+    const int slot = blockIdx.y, t = slot / n_used, kk = slot - t * n_used;
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
+    const bool emit = blockIdx.x == 0 && kk == 0;
+    int e_rank = 0;
+    const bool ok = cert_select_wave(cs.ca, ra, t, false, lane, e_rank);
+    const bool certified = !__syncthreads_or(ok ? 0 : 1);   // pooled: the general path needs every wave
+    const int e = certified ? __builtin_amdgcn_readlane(e_rank, kk)
+                            : cert_select_tokens<1>(x, K, cs.w, cs.wstride, cs.ca, ra, t, emit, sel_prod)[kk];
+    gate_up_rows<GT, G, UPL, true>(x + (int64_t)t * K, slot, e, ew, K, F, 0, h);
+    if (certified && emit && wave == 0) cert_emit_any(cs.ca, ra, t, lane, e_rank);
 }
 
 // One wave per selected expert k, lane group (G lanes) per output row, UPL
@@ -172,6 +203,21 @@ hipError_t launch_decode_gate_up(const float *x, int64_t ldx, const int32_t *idx
 {
     if (ew.gate_type != ew.up_type) return hipErrorInvalidValue;
     return decode_gate_up_impl(x, ldx, idx, n_slots, n_used, ew, K, F, h, true, 0, s);
+}
+
+hipError_t launch_decode_gate_up_sel(const float *x, int T, int n_used, const ExpertWeights &ew, int K, int F,
+                                     float *h, const CertSel &cs, const RouteArgs &ra, hipStream_t s)
+{
+    if (ew.gate_type != ew.up_type || !gemv_type_ok(ew.gate_type, K) || T <= 0 || F <= 0 || ra.T != T ||
+        ra.k != n_used || ra.idx == nullptr || ra.scores == nullptr || !router_cert_ok(K, ra.E, n_used))
+        return hipErrorInvalidValue;
+    const int G = lanes_per_row(K / 32), UPL = K / 32 / G;
+    const int rows_per_wg = (DEC_TPB / WAVE) * (WAVE / G) * 2;
+    const dim3 grid((unsigned)((F + rows_per_wg - 1) / rows_per_wg), (unsigned)(T * n_used));
+    const size_t lds = (size_t)cs.ca.nb * (K + 4) * sizeof(float);
+    DS3_T_SWITCH(ew.gate_type, DS3_G_SWITCH(G, DS3_U_SWITCH(UPL, hipLaunchKernelGGL(
+        (k_decode_gate_up_sel<TV, GV, UV>), grid, dim3(DEC_TPB), lds, s, x, n_used, ew, K, F, h, cs, ra))));
+    return hipGetLastError();
 }
 
 hipError_t launch_decode_proj(const float *x, int64_t ldx, const int32_t *idx, int n_slots, int n_used,

@@ -1,0 +1,766 @@
+// route_select.h -- per-token expert selection shared by the router
+// kernels and the fused decode kernel.
+//
+// Softmax + top-k + renorm of one token by one wavefront (route_token_row),
+// and the certified router's selection of a token group by one workgroup
+// (cert_select_tokens).  Device code only; every function is inline so that
+// each translation unit carries its own copy.
+#pragma once
+#include "common.h"
+#include "launch.h"
+
+namespace ds3k {
+
+constexpr int ROUTE_MAX_E = 256;      // experts per token (4 per lane)
+constexpr int ROUTE_EPL = ROUTE_MAX_E / WAVE;
+constexpr int ROUTE_MAX_K = 32;
+
+// Wave-wide argmax of (value desc, index asc).  Every lane gets the winner.
+__device__ __forceinline__ void wave_argmax(float &v, int &i)
+{
+#pragma unroll
+    for (int o = WAVE / 2; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o, WAVE);
+        const int oi = __shfl_xor(i, o, WAVE);
+        if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+    }
+}
+
+// Order-preserving map of finite floats (and infinities) to unsigned keys.
+__device__ __forceinline__ uint32_t order_key(float v)
+{
+    const uint32_t u = __float_as_uint(v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float readlane_f(float v, int l)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Softmax + top-k + renorm of one token by one wave (wv < 4: its LDS slot)
+// from its E logits at lg; writes the k indices to oi and weights to os.  The
+// pointers may address global memory or LDS.
+__device__ inline void route_token_row(const float *lg, int E, int k, bool norm, int32_t *oi, float *os, int wv,
+                                       int lane)
+{
+    const uint64_t below = (1ull << lane) - 1ull;
+    __shared__ int cand_s[4][WAVE];
+    __shared__ float val_s[4][WAVE];
+    __shared__ float ord_v_s[4][WAVE];
+    __shared__ int ord_e_s[4][WAVE];
+
+    float l[ROUTE_EPL];
+    bool finite = true;
+#pragma unroll
+    for (int j = 0; j < ROUTE_EPL; j++) {
+        const int e = lane + WAVE * j;
+        l[j] = e < E ? lg[e] : -INFINITY;
+        if (e < E && !__builtin_isfinite(l[j])) finite = false;
+    }
+    const bool all_finite = __all(finite);
+
+    const int need = min(k + 1, E);
+
+    // Fast path: the need = min(k+1, E) largest logits by a radix select on
+    // order keys (ballot counts, no shuffles), ranked by (value desc, index
+    // asc).  A gap above 2^-19 between neighbours keeps their probabilities
+    // at least 16 ulp apart, so expf cannot tie or reorder them: the logit
+    // order is then the reference's (prob desc) order.
+    if (all_finite) {
+        uint32_t key[ROUTE_EPL];
+#pragma unroll
+        for (int j = 0; j < ROUTE_EPL; j++) key[j] = lane + WAVE * j < E ? order_key(l[j]) : 0u;
+        uint32_t thr = 0u;                      // largest key with >= need keys at or above it
+        for (int bit = 31; bit >= 0; bit--) {
+            const uint32_t tr = thr | (1u << bit);
+            int cnt = 0;
+#pragma unroll
+            for (int j = 0; j < ROUTE_EPL; j++) cnt += __popcll(__ballot(key[j] >= tr));
+            if (cnt >= need) thr = tr;
+        }
+        int S = 0;
+#pragma unroll
+        for (int j = 0; j < ROUTE_EPL; j++) {
+            const bool in = key[j] >= thr;
+            const uint64_t m = __ballot(in);
+            const int pos = S + __popcll(m & below);
+            if (in && pos < WAVE) {
+                cand_s[wv][pos] = lane + WAVE * j;
+                val_s[wv][pos] = l[j];
+            }
+            S += __popcll(m);
+        }
+        if (S <= WAVE) {                        // else: a tie wider than a wave, general path
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            float vi = 0.f;
+            int ei = 0, rank = 0;
+            if (lane < S) {
+                vi = val_s[wv][lane];
+                ei = cand_s[wv][lane];
+                for (int c = 0; c < S; c++) {
+                    const float vc = val_s[wv][c];
+                    rank += (vc > vi || (vc == vi && cand_s[wv][c] < ei)) ? 1 : 0;
+                }
+            }
+            if (lane < S) {
+                ord_v_s[wv][rank] = vi;
+                ord_e_s[wv][rank] = ei;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            const float my_v = lane < need ? ord_v_s[wv][lane] : 0.f;
+            const int my_e = lane < need ? ord_e_s[wv][lane] : 0;
+            const float prev_v = (lane >= 1 && lane < need) ? ord_v_s[wv][lane - 1] : 0.f;
+            const bool ok = lane == 0 || lane >= need || prev_v - my_v > 0x1.0p-19f;
+            if (__all(ok)) {
+                const float mx = ord_v_s[wv][0];
+                float sp = 0.f;
+#pragma unroll
+                for (int j = 0; j < ROUTE_EPL; j++)
+                    if (lane + WAVE * j < E) sp += expf(l[j] - mx);
+                const float inv = 1.0f / wave_sum(sp);
+                const float p = expf(my_v - mx) * inv;
+                float ssum = 0.f;
+                for (int r = 0; r < k; r++) ssum += readlane_f(p, r);     // sequential, in k order
+                if (lane < k) {
+                    float w = p;
+                    if (norm && ssum > 0.0f) w *= 1.0f / ssum;
+                    oi[lane] = my_e;
+                    os[lane] = w;
+                }
+                return;                         // uniform over the wave
+            }
+        }
+    }
+
+    // General path: close logits, non-finite logits, wide ties.  Softmax.
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < ROUTE_EPL; j++) mx = fmaxf(mx, l[j]);
+    mx = wave_max(mx);
+    float p[ROUTE_EPL];
+    float sp = 0.f;
+#pragma unroll
+    for (int j = 0; j < ROUTE_EPL; j++) {
+        const int e = lane + WAVE * j;
+        p[j] = e < E ? expf(l[j] - mx) : 0.f;
+        sp += p[j];
+    }
+    const float inv = 1.0f / wave_sum(sp);
+#pragma unroll
+    for (int j = 0; j < ROUTE_EPL; j++) p[j] *= inv;
+
+    // Top-k by (prob desc, index asc).
+    float sel_v = 0.f, ssum = 0.f;
+    int sel_i = 0;
+    for (int r = 0; r < k; r++) {
+        float bv = -1.0f;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < ROUTE_EPL; j++) {
+            const int e = lane + WAVE * j;
+            // a NaN probability ranks below every number but stays selectable,
+            // so each round always yields an index < E (k <= E)
+            const float key = (p[j] == p[j]) ? p[j] : -0.5f;
+            if (e < E && key > -1.5f && (key > bv || (key == bv && e < bi))) { bv = key; bi = e; }
+        }
+        wave_argmax(bv, bi);
+        if ((bi & (WAVE - 1)) == lane) {                      // remove from later rounds
+#pragma unroll
+            for (int j = 0; j < ROUTE_EPL; j++)
+                if (j == bi / WAVE) p[j] = -2.0f;
+        }
+        ssum += bv;                                           // sequential, in k order
+        if (lane == r) { sel_v = bv; sel_i = bi; }
+    }
+    if (lane < k) {
+        float w = sel_v;
+        if (norm && ssum > 0.0f) w *= 1.0f / ssum;
+        oi[lane] = sel_i;
+        os[lane] = w;
+    }
+}
+
+// Softmax + top-k + renorm of token t of a by one wave.
+__device__ inline void route_token(const RouteArgs &a, int t, int wv, int lane)
+{
+    route_token_row(a.logits + (int64_t)t * a.logit_stride, a.E, a.k, a.norm, a.idx + (int64_t)t * a.out_stride,
+                    a.scores + (int64_t)t * a.out_stride, wv, lane);
+}
+
+// ---------------------------------------------------------------------------
+// Certified router (latency path for few tokens).
+//
+// The reference's logit is a chain of K dependent fp32 additions
+// (src/ds3_reference.c:424-434): ~K * 6 cycles of latency however many lanes
+// are free.  Instead, for each (token, expert):
+//   S = sum_i p_i in fp64, where p_i = fl32(x_i * w_i) are the reference's
+//       own rounded products (exact in fp64), and
+//   B >= |reference logit - S|, a proven bound.  The reference's k-th partial
+//       sum rounds once, |s^_k - (s^_{k-1} + p_k)| <= u |s^_k| (u = 2^-24), so
+//       |s^_K - s_K| <= u sum_k |s^_k| <= u A / (1 - K u), A = sum_k |s_k|
+//       over the exact prefix sums s_k of the p_i.  A is evaluated from the
+//       same products (lane-local prefixes, a wavefront scan, the workgroup's
+//       wave totals) and inflated by a bound on its own rounding; the host
+//       folds every constant into bfac (router_cert_bfac):
+//       B = bfac * A_computed + 1e-35.
+// k_router_sums: one workgroup per (token group, expert), each of its 4
+// waves sums a quarter of K, so one memory round trip brings every operand.
+// k_router_select: one workgroup per token group ranks the experts by
+// (fl32(S) desc, index asc), then certifies the top k: every adjacent pair
+// in that order, and the k-th against every other expert, must be separated
+// by more than B_a + B_b + tau, where tau covers the reference's softmax
+// roundings (l - max, expf, the normalisation; src/ds3_reference.c:344-359)
+// so that its probabilities order the same way, strictly.  A certified
+// token's top k, in order, is the reference's, and its weights come from
+// the fl32(S) logits.  A token that fails (about 2 % at N(0, 0.02) routers)
+// is repaired: every expert that could still reach the top k gets the
+// reference's exact sequential chain, then the ordinary selection runs on
+// the repaired row.
+// ---------------------------------------------------------------------------
+constexpr int RC_WAVES = 4;
+constexpr int RC_THREADS = 64 * RC_WAVES;
+
+// DPP lane moves: row_shr:n inside rows of 16 lanes, row_bcast:15 / :31,
+// wave_shr:1.  Lanes without a source lane read 0.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ double dpp_d(double v)
+{
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROW_MASK, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROW_MASK, 0xf, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Inclusive prefix sum over the wavefront: four row_shr steps inside each
+// row of 16, then rows 1 and 3 add lane 15 of the row below, rows 2 and 3
+// lane 31.  Every result is a tree of at most 6 additions.
+__device__ __forceinline__ float wave_incl_scan(float v)
+{
+    v = v + dpp_f<0x111>(v);
+    v = v + dpp_f<0x112>(v);
+    v = v + dpp_f<0x114>(v);
+    v = v + dpp_f<0x118>(v);
+    v = v + dpp_f<0x142, 0xa>(v);
+    v = v + dpp_f<0x143, 0xc>(v);
+    return v;
+}
+
+__device__ __forceinline__ double wave_incl_scan_f64(double v)
+{
+    v = v + dpp_d<0x111>(v);
+    v = v + dpp_d<0x112>(v);
+    v = v + dpp_d<0x114>(v);
+    v = v + dpp_d<0x118>(v);
+    v = v + dpp_d<0x142, 0xa>(v);
+    v = v + dpp_d<0x143, 0xc>(v);
+    return v;
+}
+
+__device__ __forceinline__ double readlane_d(double v, int l)
+{
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Spacing of fp32 numbers at magnitude m: 2^(e - 23) for m in [2^e, 2^(e+1)).
+__device__ __forceinline__ double f32_ulp(double m)
+{
+    const float f = (float)fmax(m, 1e-30);
+    return (double)ldexpf(1.0f, ilogbf(f) - 23);
+}
+
+// Order-preserving unsigned key of a double (larger value, larger key).
+__device__ __forceinline__ unsigned long long order_key_d(double v)
+{
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    return (u & 0x8000000000000000ull) ? ~u : (u | 0x8000000000000000ull);
+}
+
+// L contiguous floats at p (16-, 8- or 4-byte loads as L allows).
+template <int L>
+__device__ __forceinline__ void load_run(const float *p, float (&v)[L])
+{
+    if constexpr (L % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < L; i += 4) {
+            const float4 q = *(const float4 *)(p + i);
+            v[i] = q.x; v[i + 1] = q.y; v[i + 2] = q.z; v[i + 3] = q.w;
+        }
+    } else if constexpr (L % 2 == 0) {
+#pragma unroll
+        for (int i = 0; i < L; i += 2) {
+            const float2 q = *(const float2 *)(p + i);
+            v[i] = q.x; v[i + 1] = q.y;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < L; i++) v[i] = p[i];
+    }
+}
+
+// Emit the k selected experts of a token from its fp32 logits (l: this
+// lane's experts lane + 64 j) in the order given by (my_e, my_v) of lanes
+// 0..k-1: the reference's softmax over all E logits, top-k values,
+// renormalisation (src/ds3_reference.c:344-359, 632-639).
+__device__ __forceinline__ void emit_ranked(const RouteArgs &a, int t, const float (&l)[ROUTE_EPL], float my_v,
+                                            float mx, int my_e, int lane)
+{
+    const int E = a.E;
+    float sp = 0.f;
+#pragma unroll
+    for (int j = 0; j < ROUTE_EPL; j++)
+        if (lane + WAVE * j < E) sp += expf(l[j] - mx);
+    const float inv = 1.0f / wave_sum(sp);
+    const float p = expf(my_v - mx) * inv;
+    float ssum = 0.f;
+    for (int r = 0; r < a.k; r++) ssum += readlane_f(p, r);     // sequential, in k order
+    if (lane < a.k) {
+        float wt = p;
+        if (a.norm && ssum > 0.0f) wt *= 1.0f / ssum;
+        a.idx[(int64_t)t * a.out_stride + lane] = my_e;
+        a.scores[(int64_t)t * a.out_stride + lane] = wt;
+    }
+}
+
+// Exact reference chains for the candidate experts of token t (the whole
+// workgroup): the products of nb candidates at a time go to LDS, then lane m
+// of wave 0 adds candidate m's in order and overwrites its logit.
+__device__ inline void cert_repair(const float *__restrict__ x, int K, const float *__restrict__ w, int64_t wstride,
+                            int t, const uint64_t (&cand)[4], float *logits_row, int nb, float *prod)
+{
+#pragma clang fp contract(off)
+    __shared__ int list_s[ROUTE_MAX_E];
+    __shared__ int n_s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    {
+        const uint64_t m = cand[wave];
+        int pre = 0;
+        for (int j = 0; j < wave; j++) pre += __popcll(cand[j]);
+        if ((m >> lane) & 1ull) list_s[pre + __popcll(m & ((1ull << lane) - 1ull))] = tid;
+        if (tid == 0) n_s = __popcll(cand[0]) + __popcll(cand[1]) + __popcll(cand[2]) + __popcll(cand[3]);
+    }
+    __syncthreads();
+    const int n = n_s;
+    const int rowf = K + 4;
+    const float *xr = x + (int64_t)t * K;
+    for (int b0 = 0; b0 < n; b0 += nb) {
+        const int nbb = min(nb, n - b0);
+        for (int m = wave; m < nbb; m += RC_WAVES) {
+            const float *wr = w + (int64_t)list_s[b0 + m] * wstride;
+            for (int i = 4 * lane; i < K; i += 4 * WAVE) {
+                const float4 wq = *(const float4 *)(wr + i), xq = *(const float4 *)(xr + i);
+                float4 p;
+                p.x = xq.x * wq.x;
+                p.y = xq.y * wq.y;
+                p.z = xq.z * wq.z;
+                p.w = xq.w * wq.w;
+                *(float4 *)(prod + (int64_t)m * rowf + i) = p;
+            }
+        }
+        __syncthreads();
+        if (tid < nbb) {
+            const float *pr = prod + (int64_t)tid * rowf;
+            float acc = 0.0f;
+            for (int i = 0; i < K; i += 16) {
+                float4 v[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) v[q] = *(const float4 *)(pr + i + 4 * q);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    acc = acc + v[q].x;
+                    acc = acc + v[q].y;
+                    acc = acc + v[q].z;
+                    acc = acc + v[q].w;
+                }
+            }
+            logits_row[list_s[b0 + tid]] = acc;
+        }
+        __syncthreads();
+    }
+}
+
+// DPP moves whose lanes without a source (and rows outside ROW_MASK) keep
+// `old`: the identity of the reduction.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_fo(float v, float old)
+{
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ double dpp_do(double v, double old)
+{
+    const uint64_t b = __builtin_bit_cast(uint64_t, v), o = __builtin_bit_cast(uint64_t, old);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)o, (int)(uint32_t)b, CTRL, ROW_MASK,
+                                                              0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp((int)(uint32_t)(o >> 32), (int)(uint32_t)(b >> 32),
+                                                              CTRL, ROW_MASK, 0xf, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Wavefront max (the same scan pattern as wave_incl_scan; lane 63 holds it).
+__device__ __forceinline__ float wave_max_dpp(float v)
+{
+    v = fmaxf(v, dpp_fo<0x111>(v, -INFINITY));
+    v = fmaxf(v, dpp_fo<0x112>(v, -INFINITY));
+    v = fmaxf(v, dpp_fo<0x114>(v, -INFINITY));
+    v = fmaxf(v, dpp_fo<0x118>(v, -INFINITY));
+    v = fmaxf(v, dpp_fo<0x142, 0xa>(v, -INFINITY));
+    v = fmaxf(v, dpp_fo<0x143, 0xc>(v, -INFINITY));
+    return readlane_f(v, 63);
+}
+
+__device__ __forceinline__ double wave_max_dpp_d(double v)
+{
+    v = fmax(v, dpp_do<0x111>(v, -INFINITY));
+    v = fmax(v, dpp_do<0x112>(v, -INFINITY));
+    v = fmax(v, dpp_do<0x114>(v, -INFINITY));
+    v = fmax(v, dpp_do<0x118>(v, -INFINITY));
+    v = fmax(v, dpp_do<0x142, 0xa>(v, -INFINITY));
+    v = fmax(v, dpp_do<0x143, 0xc>(v, -INFINITY));
+    return readlane_d(v, 63);
+}
+
+// Wavefront max of unsigned values (lanes without a source read 0).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
+{
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Outputs of a certified token t from its ranking (lane r < k: expert
+// e_rank of rank r; the fl32(S) logits): the reference's softmax over all E
+// logits, the top-k values, renormalisation (src/ds3_reference.c:344-359,
+// 632-639); writes idx / scores and counts the token.  One wavefront.
+template <int EPL>
+__device__ inline void cert_emit(const CertArgs &ca, const RouteArgs &a, int t, int lane, int e_rank)
+{
+    const int E = a.E, k = a.k;
+    const double *Srow = ca.S + (int64_t)t * E;
+    float lf[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; j++) lf[j] = (float)Srow[min(lane + WAVE * j, E - 1)];
+    const float my_v = (float)Srow[lane < k ? e_rank : 0];
+    const float mx = readlane_f(my_v, 0);
+    float sp = 0.f;
+#pragma unroll
+    for (int j = 0; j < EPL; j++)
+        if (lane + WAVE * j < E) sp += expf(lf[j] - mx);
+    const float inv = 1.0f / readlane_f(wave_incl_scan(sp), 63);
+    const float p = expf(my_v - mx) * inv;
+    float ssum = 0.f;
+    for (int r = 0; r < k; r++) ssum += readlane_f(p, r);     // sequential, in k order
+    if (lane < k) {
+        float wt = p;
+        if (a.norm && ssum > 0.0f) wt *= 1.0f / ssum;
+        a.idx[(int64_t)t * a.out_stride + lane] = e_rank;
+        a.scores[(int64_t)t * a.out_stride + lane] = wt;
+    }
+    if (lane == 0 && ca.stats != nullptr) atomicAdd(&ca.stats[0], 1ull);
+}
+
+__device__ inline void cert_emit_any(const CertArgs &ca, const RouteArgs &a, int t, int lane, int e_rank)
+{
+    switch ((a.E + WAVE - 1) / WAVE) {                // uniform
+    case 1: cert_emit<1>(ca, a, t, lane, e_rank); break;
+    case 2: cert_emit<2>(ca, a, t, lane, e_rank); break;
+    case 3: cert_emit<3>(ca, a, t, lane, e_rank); break;
+    default: cert_emit<4>(ca, a, t, lane, e_rank); break;
+    }
+}
+
+// The certified selection of token t by one wavefront, in registers: no
+// workgroup barrier, no LDS -- the common case of cert_select_tokens.  Lane
+// l holds experts l + 64 j (EPL of them).  k rounds of a wavefront max over
+// 32-bit keys (the order key of fl32(S) with its low 8 bits replaced by
+// 255 - e) give the top k in order with no search for the winner; the
+// truncation can only put experts within 256 ulps of each other out of
+// order, and any such pair fails the certification test below (their bounds
+// overlap by far more), which is that of cert_select_tokens.  Returns
+// whether the token is certified (wave-uniform); if so, lane r < k gets the
+// expert of rank r in e_rank and, with emit, the token's idx / scores are
+// written and counted.  A token with a non-finite value, or one that fails
+// the test, returns false and is left to cert_select_tokens.
+template <int EPL>
+__device__ inline bool cert_select_wave_e(const CertArgs &ca, const RouteArgs &a, int t, bool emit, int lane,
+                                          int &e_rank)
+{
+    const int E = a.E, k = a.k;
+    const double *Srow = ca.S + (int64_t)t * E;
+    const float *Brow = ca.B + (int64_t)t * E;
+    double s[EPL];
+    float b[EPL], lf[EPL];
+    uint32_t key[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {                   // every load issued before any use
+        const int e = min(lane + WAVE * j, E - 1);
+        s[j] = Srow[e];
+        b[j] = Brow[e];
+    }
+    bool fin = true;
+    uint32_t sm = 0u, bm = 0u;                        // max |fl32(S)| and max B as bit patterns (both >= 0)
+#pragma unroll
+    for (int j = 0; j < EPL; j++) {
+        const int e = lane + WAVE * j;
+        const bool v = e < E;
+        lf[j] = (float)s[j];
+        if (v && (!__builtin_isfinite(s[j]) || !__builtin_isfinite(b[j]) || !__builtin_isfinite(lf[j]))) fin = false;
+        key[j] = v ? (order_key(lf[j]) & 0xffffff00u) | (uint32_t)(255 - e) : 0u;   // > 0 when present
+        sm = max(sm, v ? __float_as_uint(fabsf(lf[j])) : 0u);
+        bm = max(bm, v ? __float_as_uint(b[j]) : 0u);
+    }
+    if (!__all(fin)) return false;
+    // k rounds: the largest remaining key; rank r's expert goes to lane r, its successor's to lane r - 1
+    int my_e = 0, nx_e = 0;
+    for (int r = 0; r < k; r++) {
+        uint32_t m = key[0];
+#pragma unroll
+        for (int j = 1; j < EPL; j++) m = max(m, key[j]);
+        m = wave_max_u32(m);
+        const int e = 255 - (int)(m & 255u);
+        my_e = lane == r ? e : my_e;
+        nx_e = lane + 1 == r ? e : nx_e;
+#pragma unroll
+        for (int j = 0; j < EPL; j++)
+            if (lane + WAVE * j == e) key[j] = 0u;
+    }
+    const int le = lane < k ? my_e : 0, ln = lane + 1 < k ? nx_e : 0;
+    const double my_s = Srow[le], nx_s = Srow[ln];      // cached: read a moment ago
+    const float my_b = Brow[le], nx_b = Brow[ln];
+    // the best of the rest: max of S + B over the experts not taken
+    double hv = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < EPL; j++)
+        if (key[j] != 0u) hv = fmax(hv, s[j] + (double)b[j]);
+    const double hi = wave_max_dpp_d(hv);
+    const double bmax = (double)__uint_as_float(wave_max_u32(bm));
+    const double ulp2 = 2.0 * f32_ulp((double)__uint_as_float(wave_max_u32(sm)));
+    const double s_top = readlane_d(my_s, 0), b_top = (double)readlane_f(my_b, 0);
+    bool ok = true;
+    if (lane < k) {
+        double lo, sb;
+        if (lane + 1 < k) {
+            sb = nx_s;
+            lo = nx_s + (double)nx_b;
+        } else {
+            sb = hi;
+            lo = hi;
+        }
+        const double span = (sb > -INFINITY ? s_top - sb : 0.0) + b_top + bmax;
+        const double tau = 0x1.0p-18 + ulp2 + 0x1.0p-23 * span;
+        ok = my_s - (double)my_b > lo + tau && s_top - my_s < 64.0;
+    }
+    if (!__all(ok)) return false;
+    e_rank = my_e;
+    if (emit) cert_emit<EPL>(ca, a, t, lane, my_e);
+    return true;
+}
+
+__device__ inline bool cert_select_wave(const CertArgs &ca, const RouteArgs &a, int t, bool emit, int lane,
+                                        int &e_rank)
+{
+    switch ((a.E + WAVE - 1) / WAVE) {                // uniform
+    case 1: return cert_select_wave_e<1>(ca, a, t, emit, lane, e_rank);
+    case 2: return cert_select_wave_e<2>(ca, a, t, emit, lane, e_rank);
+    case 3: return cert_select_wave_e<3>(ca, a, t, emit, lane, e_rank);
+    default: return cert_select_wave_e<4>(ca, a, t, emit, lane, e_rank);
+    }
+}
+
+// Rank, certify and, where needed, repair the routing of tokens t0 ..
+// t0 + TG - 1 with the whole workgroup (RC_THREADS threads, all of which call
+// it).  Returns the LDS array [TG][WAVE] whose entries 0 .. k-1 of row tt are
+// the experts of token t0 + tt in the reference's order.  With emit it also
+// writes the token's idx / scores (and repaired logits) through a and counts
+// ca.stats; without, it writes LDS only, so any number of workgroups may
+// route the same tokens.  prod: ca.nb LDS rows of K + 4 floats.
+template <int TG>
+__device__ inline const int *cert_select_tokens(const float *__restrict__ x, int K, const float *__restrict__ w,
+                                                int64_t wstride, const CertArgs &ca, const RouteArgs &a, int t0,
+                                                bool emit, float *prod)
+{
+    __shared__ double sS[TG][ROUTE_MAX_E];
+    __shared__ float sB[TG][ROUTE_MAX_E];
+    __shared__ __attribute__((aligned(16))) unsigned long long key_s[TG][ROUTE_MAX_E];
+    __shared__ int rank_s[TG][ROUTE_MAX_E];
+    __shared__ uint8_t sel_s[TG][ROUTE_MAX_E];
+    __shared__ int ord_s[TG][WAVE];
+    __shared__ float lg_s[TG][ROUTE_MAX_E];     // logits; exact chains for repaired candidates
+    __shared__ float wt_s[TG][WAVE];
+    __shared__ unsigned int bmax_s[TG];
+    __shared__ unsigned long long smax_s[TG], hi_s[TG];
+    __shared__ int bad_s[TG], fail_s[TG];
+    __shared__ uint64_t cand_s[TG][4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int E = a.E, k = a.k, T = a.T;
+    constexpr int PER = (TG * ROUTE_MAX_E + RC_THREADS - 1) / RC_THREADS;
+    const int E32 = (E + 31) & ~31;             // key rows padded with zero keys (below every expert)
+    if (tid < TG) {
+        bmax_s[tid] = 0u;
+        smax_s[tid] = 0ull;
+        hi_s[tid] = 0ull;                   // below every key: no other expert
+        bad_s[tid] = 0;
+        fail_s[tid] = 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < PER; r++) {
+        const int p = tid + RC_THREADS * r, tt = p / E, e = p - tt * E;
+        if (tt >= TG || t0 + tt >= T) continue;
+        const double s = ca.S[(int64_t)(t0 + tt) * E + e];
+        const float b = ca.B[(int64_t)(t0 + tt) * E + e];
+        const float lf = (float)s;
+        sS[tt][e] = s;
+        sB[tt][e] = b;
+        lg_s[tt][e] = lf;
+        sel_s[tt][e] = 0;
+        rank_s[tt][e] = 0;
+        key_s[tt][e] = ((unsigned long long)order_key(lf) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)e);
+        if (!__builtin_isfinite(s) || !__builtin_isfinite(b) || !__builtin_isfinite(lf)) bad_s[tt] = 1;
+        atomicMax(&bmax_s[tt], __float_as_uint(b));
+        atomicMax(&smax_s[tt], __builtin_bit_cast(unsigned long long, fabs(s)));
+    }
+    __syncthreads();
+    if (E32 > E)
+        for (int q = tid; q < TG * (E32 - E); q += RC_THREADS) key_s[q / (E32 - E)][E + q % (E32 - E)] = 0ull;
+    __syncthreads();
+    // rank by (fl32(S) desc, index asc): the number of larger keys, counted
+    // by `sub` threads per (token, expert) over E32 / sub keys each, 8 keys
+    // (four 16-byte LDS reads) at a time
+    {
+        int sub = 1;
+        while (sub < 4 && TG * E * sub * 2 <= RC_THREADS) sub *= 2;
+        const int span = E32 / sub;
+        for (int q = tid; q < TG * E * sub; q += RC_THREADS) {
+            const int pr = q / sub, part = q - pr * sub, tt = pr / E, e = pr - tt * E;
+            if (t0 + tt >= T) continue;
+            const unsigned long long my = key_s[tt][e];
+            int cnt = 0;
+            for (int c = part * span; c < (part + 1) * span; c += 8) {
+                const ulonglong2 *kp = (const ulonglong2 *)&key_s[tt][c];
+                ulonglong2 v[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = kp[i];
+#pragma unroll
+                for (int i = 0; i < 4; i++) cnt += (v[i].x > my ? 1 : 0) + (v[i].y > my ? 1 : 0);
+            }
+            atomicAdd(&rank_s[tt][e], cnt);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < PER; r++) {
+        const int p = tid + RC_THREADS * r, tt = p / E, e = p - tt * E;
+        if (tt >= TG || t0 + tt >= T) continue;
+        const int rank = rank_s[tt][e];
+        if (rank < k) {
+            ord_s[tt][rank] = e;
+            sel_s[tt][e] = 1;
+        } else {
+            atomicMax(&hi_s[tt], order_key_d(sS[tt][e] + (double)sB[tt][e]));
+        }
+    }
+    __syncthreads();
+    if (wave < TG && t0 + wave < T) {
+        const int tt = wave, t = t0 + tt;
+        const double bmax = (double)__uint_as_float(bmax_s[tt]);
+        const double ulp2 = 2.0 * f32_ulp(__builtin_bit_cast(double, smax_s[tt]));
+        const unsigned long long hk = hi_s[tt];
+        const double hi = hk == 0ull ? -INFINITY
+                                     : __builtin_bit_cast(double, (hk & 0x8000000000000000ull) ? (hk & ~0x8000000000000000ull)
+                                                                                               : ~hk);
+        const int e_top = ord_s[tt][0];
+        const double s_top = sS[tt][e_top], b_top = sB[tt][e_top];
+        bool ok = !bad_s[tt];
+        double tau_k = 0.0;
+        int my_e = 0;
+        if (lane < k) {
+            my_e = ord_s[tt][lane];
+            const double sa = sS[tt][my_e], ba = sB[tt][my_e];
+            double lo, sb;
+            if (lane + 1 < k) {
+                const int eb = ord_s[tt][lane + 1];
+                sb = sS[tt][eb];
+                lo = sb + (double)sB[tt][eb];
+            } else {
+                sb = hi;
+                lo = hi;
+            }
+            const double span = (sb > -INFINITY ? s_top - sb : 0.0) + b_top + bmax;
+            const double tau = 0x1.0p-18 + ulp2 + 0x1.0p-23 * span;
+            // strictly separated, and the reference's expf of l - max stays normal
+            ok = ok && sa - ba > lo + tau && s_top - sa < 64.0;
+            if (lane + 1 == k) tau_k = tau;
+        }
+        const bool certified = __all(ok);
+        if (emit && lane == 0 && ca.stats != nullptr) atomicAdd(&ca.stats[certified ? 0 : 1], 1ull);
+        float l[ROUTE_EPL];
+#pragma unroll
+        for (int j = 0; j < ROUTE_EPL; j++) {
+            const int e = lane + WAVE * j;
+            l[j] = e < E ? (float)sS[tt][e] : -INFINITY;
+        }
+        if (certified) {
+            if (emit) emit_ranked(a, t, l, lane < k ? (float)sS[tt][my_e] : 0.f, (float)s_top, my_e, lane);
+        } else {
+            // candidates: the top k, and every expert whose interval reaches
+            // the k-th's (all experts when some value is not finite)
+            tau_k = readlane_d(tau_k, k - 1);
+            const double thr = sS[tt][ord_s[tt][k - 1]] - bmax - ulp2 - tau_k - 0x1.0p-18;
+            const bool all = bad_s[tt] != 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int e = lane + WAVE * j;
+                const bool in = e < E && (all || sel_s[tt][e] || sS[tt][e] + (double)sB[tt][e] >= thr);
+                const uint64_t m = __ballot(in);
+                if (lane == 0) cand_s[tt][j] = m;
+            }
+            if (lane == 0) fail_s[tt] = 1;
+        }
+    }
+    __syncthreads();
+    bool any = false;
+    for (int tt = 0; tt < TG; tt++) {
+        if (!fail_s[tt]) continue;                          // uniform over the workgroup
+        any = true;
+        const uint64_t cand[4] = { cand_s[tt][0], cand_s[tt][1], cand_s[tt][2], cand_s[tt][3] };
+        cert_repair(x, K, w, wstride, t0 + tt, cand, lg_s[tt], ca.nb, prod);
+    }
+    if (any) {
+        if (wave < TG && fail_s[wave]) {
+            const int t = t0 + wave;
+            route_token_row(lg_s[wave], E, k, a.norm, ord_s[wave], wt_s[wave], wave, lane);
+            if (emit) {
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                if (lane < k) {
+                    a.idx[(int64_t)t * a.out_stride + lane] = ord_s[wave][lane];
+                    a.scores[(int64_t)t * a.out_stride + lane] = wt_s[wave][lane];
+                }
+                float *lrow = (float *)a.logits + (int64_t)t * a.logit_stride;
+                for (int e = lane; e < E; e += WAVE) lrow[e] = lg_s[wave][e];
+            }
+        }
+        __syncthreads();
+    }
+    return &ord_s[0][0];
+}
+
+}  // namespace ds3k

@@ -14,25 +14,9 @@
 // renorm): probabilities exp(l - max) / sum, k rounds of selection by (prob
 // desc, index asc), then weights divided by their sum.  One wavefront per
 // token.
-#include "common.h"
-#include "launch.h"
+#include "route_select.h"
 
 namespace ds3k {
-
-constexpr int ROUTE_MAX_E = 256;      // experts per token (4 per lane)
-constexpr int ROUTE_EPL = ROUTE_MAX_E / WAVE;
-constexpr int ROUTE_MAX_K = 32;
-
-// Wave-wide argmax of (value desc, index asc).  Every lane gets the winner.
-__device__ __forceinline__ void wave_argmax(float &v, int &i)
-{
-#pragma unroll
-    for (int o = WAVE / 2; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(v, o, WAVE);
-        const int oi = __shfl_xor(i, o, WAVE);
-        if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
-    }
-}
 
 // Element i of one router row as the reference's FP32 copy holds it
 // (src/ds3_reference.c:87-184: the same products and roundings, no fusion).
@@ -358,8 +342,6 @@ __device__ __forceinline__ void rsm_sum(float &acc, const u32x4 (&v)[4])
         for (int j = 0; j < 4; j++) acc = acc + __uint_as_float(v[i][j]);
 }
 
-__device__ void route_token(const RouteArgs &a, int t, int wv, int lane);
-
 template <int EPW>
 __global__ void __launch_bounds__(192)
 k_router_small(const float *__restrict__ x, int T, int K, int E, const float *__restrict__ w, int64_t wstride,
@@ -494,164 +476,6 @@ k_router_small(const float *__restrict__ x, int T, int K, int E, const float *__
     }
 }
 
-// Order-preserving map of finite floats (and infinities) to unsigned keys.
-__device__ __forceinline__ uint32_t order_key(float v)
-{
-    const uint32_t u = __float_as_uint(v);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ float readlane_f(float v, int l)
-{
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
-}
-
-// Softmax + top-k + renorm of token t by one wave (wv < 4: its LDS slot).
-__device__ void route_token(const RouteArgs &a, int t, int wv, int lane)
-{
-    const int E = a.E;
-    const uint64_t below = (1ull << lane) - 1ull;
-    __shared__ int cand_s[4][WAVE];
-    __shared__ float val_s[4][WAVE];
-    __shared__ float ord_v_s[4][WAVE];
-    __shared__ int ord_e_s[4][WAVE];
-
-    float l[ROUTE_EPL];
-    const float *lg = a.logits + (int64_t)t * a.logit_stride;
-    bool finite = true;
-#pragma unroll
-    for (int j = 0; j < ROUTE_EPL; j++) {
-        const int e = lane + WAVE * j;
-        l[j] = e < E ? lg[e] : -INFINITY;
-        if (e < E && !__builtin_isfinite(l[j])) finite = false;
-    }
-    const bool all_finite = __all(finite);
-
-    int32_t *oi = a.idx + (int64_t)t * a.out_stride;
-    float *os = a.scores + (int64_t)t * a.out_stride;
-    const int need = min(a.k + 1, E);
-
-    // Fast path: the need = min(k+1, E) largest logits by a radix select on
-    // order keys (ballot counts, no shuffles), ranked by (value desc, index
-    // asc).  A gap above 2^-19 between neighbours keeps their probabilities
-    // at least 16 ulp apart, so expf cannot tie or reorder them: the logit
-    // order is then the reference's (prob desc) order.
-    if (all_finite) {
-        uint32_t key[ROUTE_EPL];
-#pragma unroll
-        for (int j = 0; j < ROUTE_EPL; j++) key[j] = lane + WAVE * j < E ? order_key(l[j]) : 0u;
-        uint32_t thr = 0u;                      // largest key with >= need keys at or above it
-        for (int bit = 31; bit >= 0; bit--) {
-            const uint32_t tr = thr | (1u << bit);
-            int cnt = 0;
-#pragma unroll
-            for (int j = 0; j < ROUTE_EPL; j++) cnt += __popcll(__ballot(key[j] >= tr));
-            if (cnt >= need) thr = tr;
-        }
-        int S = 0;
-#pragma unroll
-        for (int j = 0; j < ROUTE_EPL; j++) {
-            const bool in = key[j] >= thr;
-            const uint64_t m = __ballot(in);
-            const int pos = S + __popcll(m & below);
-            if (in && pos < WAVE) {
-                cand_s[wv][pos] = lane + WAVE * j;
-                val_s[wv][pos] = l[j];
-            }
-            S += __popcll(m);
-        }
-        if (S <= WAVE) {                        // else: a tie wider than a wave, general path
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            float vi = 0.f;
-            int ei = 0, rank = 0;
-            if (lane < S) {
-                vi = val_s[wv][lane];
-                ei = cand_s[wv][lane];
-                for (int c = 0; c < S; c++) {
-                    const float vc = val_s[wv][c];
-                    rank += (vc > vi || (vc == vi && cand_s[wv][c] < ei)) ? 1 : 0;
-                }
-            }
-            if (lane < S) {
-                ord_v_s[wv][rank] = vi;
-                ord_e_s[wv][rank] = ei;
-            }
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            const float my_v = lane < need ? ord_v_s[wv][lane] : 0.f;
-            const int my_e = lane < need ? ord_e_s[wv][lane] : 0;
-            const float prev_v = (lane >= 1 && lane < need) ? ord_v_s[wv][lane - 1] : 0.f;
-            const bool ok = lane == 0 || lane >= need || prev_v - my_v > 0x1.0p-19f;
-            if (__all(ok)) {
-                const float mx = ord_v_s[wv][0];
-                float sp = 0.f;
-#pragma unroll
-                for (int j = 0; j < ROUTE_EPL; j++)
-                    if (lane + WAVE * j < E) sp += expf(l[j] - mx);
-                const float inv = 1.0f / wave_sum(sp);
-                const float p = expf(my_v - mx) * inv;
-                float ssum = 0.f;
-                for (int r = 0; r < a.k; r++) ssum += readlane_f(p, r);     // sequential, in k order
-                if (lane < a.k) {
-                    float w = p;
-                    if (a.norm && ssum > 0.0f) w *= 1.0f / ssum;
-                    oi[lane] = my_e;
-                    os[lane] = w;
-                }
-                return;                         // uniform over the wave
-            }
-        }
-    }
-
-    // General path: close logits, non-finite logits, wide ties.  Softmax.
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < ROUTE_EPL; j++) mx = fmaxf(mx, l[j]);
-    mx = wave_max(mx);
-    float p[ROUTE_EPL];
-    float sp = 0.f;
-#pragma unroll
-    for (int j = 0; j < ROUTE_EPL; j++) {
-        const int e = lane + WAVE * j;
-        p[j] = e < E ? expf(l[j] - mx) : 0.f;
-        sp += p[j];
-    }
-    const float inv = 1.0f / wave_sum(sp);
-#pragma unroll
-    for (int j = 0; j < ROUTE_EPL; j++) p[j] *= inv;
-
-    // Top-k by (prob desc, index asc).
-    float sel_v = 0.f, ssum = 0.f;
-    int sel_i = 0;
-    for (int r = 0; r < a.k; r++) {
-        float bv = -1.0f;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int j = 0; j < ROUTE_EPL; j++) {
-            const int e = lane + WAVE * j;
-            // a NaN probability ranks below every number but stays selectable,
-            // so each round always yields an index < E (k <= E)
-            const float key = (p[j] == p[j]) ? p[j] : -0.5f;
-            if (e < E && key > -1.5f && (key > bv || (key == bv && e < bi))) { bv = key; bi = e; }
-        }
-        wave_argmax(bv, bi);
-        if ((bi & (WAVE - 1)) == lane) {                      // remove from later rounds
-#pragma unroll
-            for (int j = 0; j < ROUTE_EPL; j++)
-                if (j == bi / WAVE) p[j] = -2.0f;
-        }
-        ssum += bv;                                           // sequential, in k order
-        if (lane == r) { sel_v = bv; sel_i = bi; }
-    }
-    if (lane < a.k) {
-        float w = sel_v;
-        if (a.norm && ssum > 0.0f) w *= 1.0f / ssum;
-        oi[lane] = sel_i;
-        os[lane] = w;
-    }
-}
-
 __global__ void __launch_bounds__(256) k_route(RouteArgs a)
 {
     const int lane = threadIdx.x & (WAVE - 1);
@@ -661,131 +485,8 @@ __global__ void __launch_bounds__(256) k_route(RouteArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// Certified router (latency path for few tokens).
-//
-// The reference's logit is a chain of K dependent fp32 additions
-// (src/ds3_reference.c:424-434): ~K * 6 cycles of latency however many lanes
-// are free.  Instead, for each (token, expert):
-//   S = sum_i p_i in fp64, where p_i = fl32(x_i * w_i) are the reference's
-//       own rounded products (exact in fp64), and
-//   B >= |reference logit - S|, a proven bound.  The reference's k-th partial
-//       sum rounds once, |s^_k - (s^_{k-1} + p_k)| <= u |s^_k| (u = 2^-24), so
-//       |s^_K - s_K| <= u sum_k |s^_k| <= u A / (1 - K u), A = sum_k |s_k|
-//       over the exact prefix sums s_k of the p_i.  A is evaluated from the
-//       same products (lane-local prefixes, a wavefront scan, the workgroup's
-//       wave totals) and inflated by a bound on its own rounding; the host
-//       folds every constant into bfac (router_cert_bfac):
-//       B = bfac * A_computed + 1e-35.
-// k_router_sums: one workgroup per (token group, expert), each of its 4
-// waves sums a quarter of K, so one memory round trip brings every operand.
-// k_router_select: one workgroup per token group ranks the experts by
-// (fl32(S) desc, index asc), then certifies the top k: every adjacent pair
-// in that order, and the k-th against every other expert, must be separated
-// by more than B_a + B_b + tau, where tau covers the reference's softmax
-// roundings (l - max, expf, the normalisation; src/ds3_reference.c:344-359)
-// so that its probabilities order the same way, strictly.  A certified
-// token's top k, in order, is the reference's, and its weights come from
-// the fl32(S) logits.  A token that fails (about 2 % at N(0, 0.02) routers)
-// is repaired: every expert that could still reach the top k gets the
-// reference's exact sequential chain, then the ordinary selection runs on
-// the repaired row.
+// Certified router kernels (method and bound: route_select.h).
 // ---------------------------------------------------------------------------
-constexpr int RC_WAVES = 4;
-constexpr int RC_THREADS = 64 * RC_WAVES;
-
-struct CertArgs {
-    double *S;                   // [T][E]
-    float *B;                    // [T][E]
-    float bfac;
-    int nb;                      // candidate rows per repair batch (dynamic LDS rows of K + 4 floats)
-    unsigned long long *stats;   // optional [2]: tokens certified, tokens repaired
-};
-
-// DPP lane moves: row_shr:n inside rows of 16 lanes, row_bcast:15 / :31,
-// wave_shr:1.  Lanes without a source lane read 0.
-template <int CTRL, int ROW_MASK = 0xf>
-__device__ __forceinline__ float dpp_f(float v)
-{
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
-}
-
-template <int CTRL, int ROW_MASK = 0xf>
-__device__ __forceinline__ double dpp_d(double v)
-{
-    const uint64_t b = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, ROW_MASK, 0xf, false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, ROW_MASK, 0xf, false);
-    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
-
-// Inclusive prefix sum over the wavefront: four row_shr steps inside each
-// row of 16, then rows 1 and 3 add lane 15 of the row below, rows 2 and 3
-// lane 31.  Every result is a tree of at most 6 additions.
-__device__ __forceinline__ float wave_incl_scan(float v)
-{
-    v = v + dpp_f<0x111>(v);
-    v = v + dpp_f<0x112>(v);
-    v = v + dpp_f<0x114>(v);
-    v = v + dpp_f<0x118>(v);
-    v = v + dpp_f<0x142, 0xa>(v);
-    v = v + dpp_f<0x143, 0xc>(v);
-    return v;
-}
-
-__device__ __forceinline__ double wave_incl_scan_f64(double v)
-{
-    v = v + dpp_d<0x111>(v);
-    v = v + dpp_d<0x112>(v);
-    v = v + dpp_d<0x114>(v);
-    v = v + dpp_d<0x118>(v);
-    v = v + dpp_d<0x142, 0xa>(v);
-    v = v + dpp_d<0x143, 0xc>(v);
-    return v;
-}
-
-__device__ __forceinline__ double readlane_d(double v, int l)
-{
-    const uint64_t b = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
-    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
-
-// Spacing of fp32 numbers at magnitude m: 2^(e - 23) for m in [2^e, 2^(e+1)).
-__device__ __forceinline__ double f32_ulp(double m)
-{
-    const float f = (float)fmax(m, 1e-30);
-    return (double)ldexpf(1.0f, ilogbf(f) - 23);
-}
-
-// Order-preserving unsigned key of a double (larger value, larger key).
-__device__ __forceinline__ unsigned long long order_key_d(double v)
-{
-    const uint64_t u = __builtin_bit_cast(uint64_t, v);
-    return (u & 0x8000000000000000ull) ? ~u : (u | 0x8000000000000000ull);
-}
-
-// L contiguous floats at p (16-, 8- or 4-byte loads as L allows).
-template <int L>
-__device__ __forceinline__ void load_run(const float *p, float (&v)[L])
-{
-    if constexpr (L % 4 == 0) {
-#pragma unroll
-        for (int i = 0; i < L; i += 4) {
-            const float4 q = *(const float4 *)(p + i);
-            v[i] = q.x; v[i + 1] = q.y; v[i + 2] = q.z; v[i + 3] = q.w;
-        }
-    } else if constexpr (L % 2 == 0) {
-#pragma unroll
-        for (int i = 0; i < L; i += 2) {
-            const float2 q = *(const float2 *)(p + i);
-            v[i] = q.x; v[i + 1] = q.y;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < L; i++) v[i] = p[i];
-    }
-}
 
 // S, B and fl32(S) for TG tokens x one expert.  Lane l of wave w covers
 // elements (64 w + l) L .. + L - 1, K = 256 L.
@@ -865,246 +566,32 @@ k_router_sums(const float *__restrict__ x, int T, int K, int E, const float *__r
     }
 }
 
-// Emit the k selected experts of a token from its fp32 logits (l: this
-// lane's experts lane + 64 j) in the order given by (my_e, my_v) of lanes
-// 0..k-1: the reference's softmax over all E logits, top-k values,
-// renormalisation (src/ds3_reference.c:344-359, 632-639).
-__device__ __forceinline__ void emit_ranked(const RouteArgs &a, int t, const float (&l)[ROUTE_EPL], float my_v,
-                                            float mx, int my_e, int lane)
-{
-    const int E = a.E;
-    float sp = 0.f;
-#pragma unroll
-    for (int j = 0; j < ROUTE_EPL; j++)
-        if (lane + WAVE * j < E) sp += expf(l[j] - mx);
-    const float inv = 1.0f / wave_sum(sp);
-    const float p = expf(my_v - mx) * inv;
-    float ssum = 0.f;
-    for (int r = 0; r < a.k; r++) ssum += readlane_f(p, r);     // sequential, in k order
-    if (lane < a.k) {
-        float wt = p;
-        if (a.norm && ssum > 0.0f) wt *= 1.0f / ssum;
-        a.idx[(int64_t)t * a.out_stride + lane] = my_e;
-        a.scores[(int64_t)t * a.out_stride + lane] = wt;
-    }
-}
-
-// Exact reference chains for the candidate experts of token t (the whole
-// workgroup): the products of nb candidates at a time go to LDS, then lane m
-// of wave 0 adds candidate m's in order and overwrites its logit.
-__device__ void cert_repair(const float *__restrict__ x, int K, const float *__restrict__ w, int64_t wstride,
-                            int t, const uint64_t (&cand)[4], float *logits_row, int nb, float *prod)
-{
-#pragma clang fp contract(off)
-    __shared__ int list_s[ROUTE_MAX_E];
-    __shared__ int n_s;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    {
-        const uint64_t m = cand[wave];
-        int pre = 0;
-        for (int j = 0; j < wave; j++) pre += __popcll(cand[j]);
-        if ((m >> lane) & 1ull) list_s[pre + __popcll(m & ((1ull << lane) - 1ull))] = tid;
-        if (tid == 0) n_s = __popcll(cand[0]) + __popcll(cand[1]) + __popcll(cand[2]) + __popcll(cand[3]);
-    }
-    __syncthreads();
-    const int n = n_s;
-    const int rowf = K + 4;
-    const float *xr = x + (int64_t)t * K;
-    for (int b0 = 0; b0 < n; b0 += nb) {
-        const int nbb = min(nb, n - b0);
-        for (int m = wave; m < nbb; m += RC_WAVES) {
-            const float *wr = w + (int64_t)list_s[b0 + m] * wstride;
-            for (int i = 4 * lane; i < K; i += 4 * WAVE) {
-                const float4 wq = *(const float4 *)(wr + i), xq = *(const float4 *)(xr + i);
-                float4 p;
-                p.x = xq.x * wq.x;
-                p.y = xq.y * wq.y;
-                p.z = xq.z * wq.z;
-                p.w = xq.w * wq.w;
-                *(float4 *)(prod + (int64_t)m * rowf + i) = p;
-            }
-        }
-        __syncthreads();
-        if (tid < nbb) {
-            const float *pr = prod + (int64_t)tid * rowf;
-            float acc = 0.0f;
-            for (int i = 0; i < K; i += 16) {
-                float4 v[4];
-#pragma unroll
-                for (int q = 0; q < 4; q++) v[q] = *(const float4 *)(pr + i + 4 * q);
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    acc = acc + v[q].x;
-                    acc = acc + v[q].y;
-                    acc = acc + v[q].z;
-                    acc = acc + v[q].w;
-                }
-            }
-            logits_row[list_s[b0 + tid]] = acc;
-        }
-        __syncthreads();
-    }
-}
-
-// Rank, certify, emit (and repair) the routing of TG tokens.
+// Rank, certify, emit (and repair) the routing of TG tokens per workgroup:
+// wave w takes token t0 + w on the one-wave path; a token it cannot certify
+// goes through the whole workgroup's general path.
 template <int TG>
 __global__ void __launch_bounds__(RC_THREADS)
 k_router_select(const float *__restrict__ x, int K, const float *__restrict__ w, int64_t wstride, CertArgs ca,
                 RouteArgs a)
 {
     extern __shared__ __attribute__((aligned(16))) float rc_prod[];
-    __shared__ double sS[TG][ROUTE_MAX_E];
-    __shared__ float sB[TG][ROUTE_MAX_E];
-    __shared__ __attribute__((aligned(16))) unsigned long long key_s[TG][ROUTE_MAX_E];
-    __shared__ int rank_s[TG][ROUTE_MAX_E];
-    __shared__ uint8_t sel_s[TG][ROUTE_MAX_E];
-    __shared__ int ord_s[TG][WAVE];
-    __shared__ unsigned int bmax_s[TG];
-    __shared__ unsigned long long smax_s[TG], hi_s[TG];
-    __shared__ int bad_s[TG], fail_s[TG];
-    __shared__ uint64_t cand_s[TG][4];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int E = a.E, k = a.k, T = a.T;
+    __shared__ int fail_s[TG];
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
     const int t0 = blockIdx.x * TG;
-    constexpr int PER = (TG * ROUTE_MAX_E + RC_THREADS - 1) / RC_THREADS;
-    const int E32 = (E + 31) & ~31;             // key rows padded with zero keys (below every expert)
-    if (tid < TG) {
-        bmax_s[tid] = 0u;
-        smax_s[tid] = 0ull;
-        hi_s[tid] = 0ull;                   // below every key: no other expert
-        bad_s[tid] = 0;
-        fail_s[tid] = 0;
+    if (wave < TG) {
+        const int t = t0 + wave;
+        int e_rank;
+        const bool ok = t < a.T && cert_select_wave(ca, a, t, true, lane, e_rank);
+        if (lane == 0) fail_s[wave] = t < a.T && !ok ? 1 : 0;
     }
     __syncthreads();
-#pragma unroll
-    for (int r = 0; r < PER; r++) {
-        const int p = tid + RC_THREADS * r, tt = p / E, e = p - tt * E;
-        if (tt >= TG || t0 + tt >= T) continue;
-        const double s = ca.S[(int64_t)(t0 + tt) * E + e];
-        const float b = ca.B[(int64_t)(t0 + tt) * E + e];
-        const float lf = (float)s;
-        sS[tt][e] = s;
-        sB[tt][e] = b;
-        sel_s[tt][e] = 0;
-        rank_s[tt][e] = 0;
-        key_s[tt][e] = ((unsigned long long)order_key(lf) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)e);
-        if (!__builtin_isfinite(s) || !__builtin_isfinite(b) || !__builtin_isfinite(lf)) bad_s[tt] = 1;
-        atomicMax(&bmax_s[tt], __float_as_uint(b));
-        atomicMax(&smax_s[tt], __builtin_bit_cast(unsigned long long, fabs(s)));
-    }
-    __syncthreads();
-    if (E32 > E)
-        for (int q = tid; q < TG * (E32 - E); q += RC_THREADS) key_s[q / (E32 - E)][E + q % (E32 - E)] = 0ull;
-    __syncthreads();
-    // rank by (fl32(S) desc, index asc): the number of larger keys, counted
-    // by `sub` threads per (token, expert) over E32 / sub keys each, 8 keys
-    // (four 16-byte LDS reads) at a time
-    {
-        int sub = 1;
-        while (sub < 4 && TG * E * sub * 2 <= RC_THREADS) sub *= 2;
-        const int span = E32 / sub;
-        for (int q = tid; q < TG * E * sub; q += RC_THREADS) {
-            const int pr = q / sub, part = q - pr * sub, tt = pr / E, e = pr - tt * E;
-            if (t0 + tt >= T) continue;
-            const unsigned long long my = key_s[tt][e];
-            int cnt = 0;
-            for (int c = part * span; c < (part + 1) * span; c += 8) {
-                const ulonglong2 *kp = (const ulonglong2 *)&key_s[tt][c];
-                ulonglong2 v[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) v[i] = kp[i];
-#pragma unroll
-                for (int i = 0; i < 4; i++) cnt += (v[i].x > my ? 1 : 0) + (v[i].y > my ? 1 : 0);
-            }
-            atomicAdd(&rank_s[tt][e], cnt);
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < PER; r++) {
-        const int p = tid + RC_THREADS * r, tt = p / E, e = p - tt * E;
-        if (tt >= TG || t0 + tt >= T) continue;
-        const int rank = rank_s[tt][e];
-        if (rank < k) {
-            ord_s[tt][rank] = e;
-            sel_s[tt][e] = 1;
-        } else {
-            atomicMax(&hi_s[tt], order_key_d(sS[tt][e] + (double)sB[tt][e]));
-        }
-    }
-    __syncthreads();
-    if (wave < TG && t0 + wave < T) {
-        const int tt = wave, t = t0 + tt;
-        const double bmax = (double)__uint_as_float(bmax_s[tt]);
-        const double ulp2 = 2.0 * f32_ulp(__builtin_bit_cast(double, smax_s[tt]));
-        const unsigned long long hk = hi_s[tt];
-        const double hi = hk == 0ull ? -INFINITY
-                                     : __builtin_bit_cast(double, (hk & 0x8000000000000000ull) ? (hk & ~0x8000000000000000ull)
-                                                                                               : ~hk);
-        const int e_top = ord_s[tt][0];
-        const double s_top = sS[tt][e_top], b_top = sB[tt][e_top];
-        bool ok = !bad_s[tt];
-        double tau_k = 0.0;
-        int my_e = 0;
-        if (lane < k) {
-            my_e = ord_s[tt][lane];
-            const double sa = sS[tt][my_e], ba = sB[tt][my_e];
-            double lo, sb;
-            if (lane + 1 < k) {
-                const int eb = ord_s[tt][lane + 1];
-                sb = sS[tt][eb];
-                lo = sb + (double)sB[tt][eb];
-            } else {
-                sb = hi;
-                lo = hi;
-            }
-            const double span = (sb > -INFINITY ? s_top - sb : 0.0) + b_top + bmax;
-            const double tau = 0x1.0p-18 + ulp2 + 0x1.0p-23 * span;
-            // strictly separated, and the reference's expf of l - max stays normal
-            ok = ok && sa - ba > lo + tau && s_top - sa < 64.0;
-            if (lane + 1 == k) tau_k = tau;
-        }
-        const bool certified = __all(ok);
-        if (lane == 0 && ca.stats != nullptr) atomicAdd(&ca.stats[certified ? 0 : 1], 1ull);
-        float l[ROUTE_EPL];
-#pragma unroll
-        for (int j = 0; j < ROUTE_EPL; j++) {
-            const int e = lane + WAVE * j;
-            l[j] = e < E ? (float)sS[tt][e] : -INFINITY;
-        }
-        if (certified) {
-            emit_ranked(a, t, l, lane < k ? (float)sS[tt][my_e] : 0.f, (float)s_top, my_e, lane);
-        } else {
-            // candidates: the top k, and every expert whose interval reaches
-            // the k-th's (all experts when some value is not finite)
-            tau_k = readlane_d(tau_k, k - 1);
-            const double thr = sS[tt][ord_s[tt][k - 1]] - bmax - ulp2 - tau_k - 0x1.0p-18;
-            const bool all = bad_s[tt] != 0;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int e = lane + WAVE * j;
-                const bool in = e < E && (all || sel_s[tt][e] || sS[tt][e] + (double)sB[tt][e] >= thr);
-                const uint64_t m = __ballot(in);
-                if (lane == 0) cand_s[tt][j] = m;
-            }
-            if (lane == 0) fail_s[tt] = 1;
-        }
-    }
-    __syncthreads();
-    bool any = false;
     for (int tt = 0; tt < TG; tt++) {
-        if (!fail_s[tt]) continue;                          // uniform over the workgroup
-        any = true;
-        const uint64_t cand[4] = { cand_s[tt][0], cand_s[tt][1], cand_s[tt][2], cand_s[tt][3] };
-        cert_repair(x, K, w, wstride, t0 + tt, cand, (float *)a.logits + (int64_t)(t0 + tt) * a.logit_stride,
-                    ca.nb, rc_prod);
-    }
-    if (any) {
-        __threadfence();
+        if (!fail_s[tt]) continue;                  // uniform over the workgroup
+        cert_select_tokens<1>(x, K, w, wstride, ca, a, t0 + tt, true, rc_prod);
         __syncthreads();
-        if (wave < TG && fail_s[wave]) route_token(a, t0 + wave, wave, lane);
     }
 }
+
 
 // bfac of the certified router for rows of K = 256 L values (see above):
 // B = bfac * A_computed bounds |reference logit - S|.  0 when K is too long
@@ -1150,22 +637,39 @@ static void cert_select(const float *x, int T, int K, const float *w, int64_t ws
                        wstride, ca, ra);
 }
 
+hipError_t router_cert_sel(int T, int K, int E, int k, int rtype, const uint8_t *rw, uint64_t rstride, float *wf32,
+                           void *scratch, unsigned long long *stats, int nb, CertSel *out)
+{
+    if (T <= 0 || !router_cert_ok(K, E, k) || !router_seq_type_ok(rtype, K) || ((uintptr_t)scratch & 7) != 0)
+        return hipErrorInvalidValue;
+    const bool f32_direct = rtype == T_F32 && rstride % 16 == 0 && ((uintptr_t)rw & 15) == 0;
+    if (!f32_direct && (wf32 == nullptr || ((uintptr_t)wf32 & 15) != 0)) return hipErrorInvalidValue;
+    out->w = f32_direct ? (const float *)rw : wf32;
+    out->wstride = f32_direct ? (int64_t)(rstride / 4) : (int64_t)K;
+    CertArgs &ca = out->ca;
+    ca.S = (double *)scratch;
+    ca.B = (float *)((uint8_t *)scratch + (((size_t)T * E * sizeof(double) + 255) & ~(size_t)255));
+    ca.bfac = (float)router_cert_bfac(K);
+    ca.stats = stats;
+    ca.nb = nb < 1 ? 1 : nb;
+    return hipSuccess;
+}
+
 hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, const uint8_t *rw, uint64_t rstride,
                               float *wf32, float *logits, int64_t ldl, _Float16 *x16, const RouteArgs &ra,
                               void *scratch, unsigned long long *stats, int phases, hipStream_t s)
 {
-    if (T <= 0 || !router_cert_ok(K, E, ra.k) || !router_seq_type_ok(rtype, K) || ra.logits != logits ||
-        ra.logit_stride != ldl || ra.T != T || ra.E != E || ra.idx == nullptr)
+    if (ra.logits != logits || ra.logit_stride != ldl || ra.T != T || ra.E != E || ra.idx == nullptr)
         return hipErrorInvalidValue;
-    if (((uintptr_t)x & 15) != 0 || ((uintptr_t)x16 & 15) != 0 || ((uintptr_t)scratch & 7) != 0)
-        return hipErrorInvalidValue;
-    const float *w = (const float *)rw;
-    int64_t wstride = (int64_t)(rstride / 4);
-    const bool f32_direct = rtype == T_F32 && rstride % 16 == 0 && ((uintptr_t)rw & 15) == 0;
-    if (!f32_direct) {
-        if (wf32 == nullptr || ((uintptr_t)wf32 & 15) != 0) return hipErrorInvalidValue;
-    }
-    if (!f32_direct && (phases & 1)) {
+    if (((uintptr_t)x & 15) != 0 || ((uintptr_t)x16 & 15) != 0) return hipErrorInvalidValue;
+    // repair batch: up to 13 candidate rows (about 104 KiB of LDS) while one
+    // token group is routed, up to 4 (~32 KiB) when several workgroups share CUs
+    const int rowb = (K + 4) * (int)sizeof(float);
+    CertSel cs;
+    hipError_t e = router_cert_sel(T, K, E, ra.k, rtype, rw, rstride, wf32, scratch, stats,
+                                   T <= 4 ? min(13, 106496 / rowb) : min(4, 33792 / rowb), &cs);
+    if (e != hipSuccess) return e;
+    if ((const float *)rw != cs.w && (phases & 1)) {
         const dim3 grid((unsigned)((K + 255) / 256), (unsigned)E);
         switch (rtype) {
         case T_F32: hipLaunchKernelGGL(k_router_rows_f32<T_F32>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
@@ -1175,21 +679,10 @@ hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, co
         default: hipLaunchKernelGGL(k_router_rows_f32<T_Q6_K>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
         }
     }
-    if (!f32_direct) {
-        w = wf32;
-        wstride = K;
-    }
+    const float *w = cs.w;
+    const int64_t wstride = cs.wstride;
+    const CertArgs &ca = cs.ca;
     const int TG = T == 1 ? 1 : T == 2 ? 2 : 4;
-    CertArgs ca;
-    ca.S = (double *)scratch;
-    ca.B = (float *)((uint8_t *)scratch + (((size_t)T * E * sizeof(double) + 255) & ~(size_t)255));
-    ca.bfac = (float)router_cert_bfac(K);
-    ca.stats = stats;
-    // repair batch: up to 13 candidate rows (about 104 KiB of LDS) while one
-    // token group is routed, up to 4 (~32 KiB) when several workgroups share CUs
-    const int rowb = (K + 4) * (int)sizeof(float);
-    ca.nb = T <= 4 ? min(13, 106496 / rowb) : min(4, 33792 / rowb);
-    if (ca.nb < 1) ca.nb = 1;
 #define DS3_CERT_SUMS(LV)                                                                        \
     do {                                                                                         \
         if (TG == 1) cert_sums<LV, 1>(x, T, K, E, w, wstride, logits, ldl, x16, ca, s);          \
@@ -1216,7 +709,7 @@ hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, co
     default: return hipErrorInvalidValue;
     }
 #undef DS3_CERT_SUMS
-    hipError_t e = hipGetLastError();
+    e = hipGetLastError();
     if (e != hipSuccess || !(phases & 2)) return e;
     if (TG == 1) cert_select<1>(x, T, K, w, wstride, ca, ra, s);
     else if (TG == 2) cert_select<2>(x, T, K, w, wstride, ca, ra, s);

@@ -377,6 +377,48 @@ def test_residual_and_accumulate(hip_ready, real):
         assert_close(got - res, want, max_abs=3e-3, rel_l2=1.2e-3)
 
 
+@pytest.mark.parametrize("T", [1, 3, 15])
+def test_decode_near_ties_fused_select(hip_ready, real, T):
+    """Decode with the selection inside the gate/up kernel, on tokens it must
+    repair: router rows 3 and 5 are row 0 moved by ~1e-8 per element, and
+    every token is pushed towards row 0, so all three sit in its top k
+    within the rounding noise of a reordered sum.  Each gate/up workgroup
+    re-sums them in the reference's order; the indices, the repaired logits
+    and the outputs must match the oracle's."""
+    wr = real.wr.copy()
+    wr[3] = wr[0] + np.float32(1e-8)
+    wr[5] = wr[0] - np.float32(1.5e-8)
+    rng = np.random.default_rng(11 + T)
+    x = (rng.standard_normal((T, 2048)) + 0.1 * np.sign(wr[0])).astype(np.float32)
+    s = real.spec
+    want, oi, osc, _ = O.moe_tokens(x, wr, real.wg, real.wu, real.wd, s.n_expert, W.N_USED, s.n_ff, 16, True)
+    ol = np.stack([O.vec_matmul(x[t], wr) for t in range(T)])
+    assert ((oi == 0).any(axis=1) & (oi == 3).any(axis=1) & (oi == 5).any(axis=1)).all()
+    router = ds3.Buffer.from_array(wr)
+    xb = ds3.Buffer.from_array(x)
+    out, idx = ds3.Buffer.alloc(T * 2048 * 4), ds3.Buffer.alloc(T * W.N_USED * 4)
+    sc, lg = ds3.Buffer.alloc(T * W.N_USED * 4), ds3.Buffer.alloc(T * s.n_expert * 4)
+    out.zero()
+    print(f"  fused-select decode near ties T={T}", flush=True)
+    ds3.router_stats(reset=True)
+    ds3.moe_ffn_batch(xb, router, ds3.TYPE_F32, real.dev.experts, out, T, s.n_expert, W.N_USED,
+                      logits=lg, indices=idx, scores=sc)
+    certified, repaired = ds3.router_stats()
+    print(f"    router: {certified} certified, {repaired} repaired", flush=True)
+    assert repaired == T and certified == 0
+    gi, gs, gl = idx.read(np.int32, (T, W.N_USED)), sc.read(np.float32, (T, W.N_USED)), lg.read(np.float32, (T, 128))
+    assert np.array_equal(gi, oi)
+    assert logit_bits_differ(gl[:, [0, 3, 5]], ol[:, [0, 3, 5]]) == 0
+    assert (np.abs(gs - osc) / osc).max() < 1e-5
+    assert_close(out.read(np.float32, (T, 2048)), want, rel_l2=5e-5)
+    if T == 1:                                       # the single-token entry point takes the same path
+        o1, l1 = ds3.Buffer.alloc(2048 * 4), ds3.Buffer.alloc(128 * 4)
+        o1.zero()
+        ds3.moe_ffn(xb, router, ds3.TYPE_F32, real.dev.experts, o1, l1, s.n_expert, W.N_USED)
+        assert logit_bits_differ(l1.read(np.float32, (1, 128))[:, [0, 3, 5]], ol[:, [0, 3, 5]]) == 0
+        assert_close(o1.read(np.float32, (1, 2048)), want, rel_l2=5e-5)
+
+
 def test_decode_stack_teacher_forced_config4(hip_ready):
     """Configuration 4 in small: h <- h + MoE_l(h) through distinct layers at
     T = 1 (decode path, residual fused), each layer checked against the
