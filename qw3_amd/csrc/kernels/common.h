@@ -316,6 +316,22 @@ __device__ __forceinline__ void fma4(uint32_t x02, uint32_t x13, uint32_t mask, 
 // ---------------------------------------------------------------------------
 template <int TYPE> struct RawUnits;
 
+// First K index of the 8 weights that lane group g (lanes 16g..16g+15)
+// supplies for K-slot q (0..7) of the 256-wide K step s, in RawUnits'
+// decode_frags order: unit g + 4*(q/4), segment q%4.  The activation side of
+// an MFMA reads the same 8 positions, so both operands share the K order.
+template <int TYPE>
+__device__ __forceinline__ int slot_k0(int s, int g, int q)
+{
+    const int c = g + 4 * (q >> 2), part = q & 3;
+    if constexpr (TYPE == T_Q4_K)
+        return 256 * s + 64 * (c >> 1) + 16 * (c & 1) + 8 * (part & 1) + 32 * (part >> 1);
+    else if constexpr (TYPE == T_Q6_K)
+        return 256 * s + 128 * (c >> 2) + 32 * part + 8 * (c & 3);
+    else
+        return 256 * s + 32 * c + 8 * part;
+}
+
 // Reads from LDS by byte address through inline asm, with their own
 // s_waitcnt lgkmcnt(0) in the same statement.  The grouped kernels stream
 // weights into LDS with global_load_lds DMAs; the compiler treats any LDS

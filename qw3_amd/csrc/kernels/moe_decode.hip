@@ -18,6 +18,9 @@ __device__ __forceinline__ const uint8_t *expert_base(const uint8_t *base, const
 }
 
 constexpr int DEC_TPB = 256;
+#ifndef DS3_SEL_RPW
+#define DS3_SEL_RPW 2          // rows per lane group in the fused-selection gate/up kernel
+#endif
 
 // PAIR: h = swiglu(gate, up).  !PAIR: h = gate projection only, with expert
 // offsets from table column `which` (unfused fallback for mixed types).
@@ -26,11 +29,11 @@ constexpr int DEC_TPB = 256;
 // results dropped), so every load of a wave is issued before its first dot
 // product and the wave pays one memory round trip.  Rows of expert e for
 // routed slot `slot` (token row xt).
-template <int GT, int G, int UPL, bool PAIR>
+template <int GT, int G, int UPL, bool PAIR, int RPW = 2>
 __device__ __forceinline__ void gate_up_rows(const float *__restrict__ xt, int slot, int e, const ExpertWeights &ew,
                                              int K, int F, int which, float *__restrict__ h)
 {
-    constexpr int GPW = WAVE / G, RPW = 2;
+    constexpr int GPW = WAVE / G;
     const uint8_t *wg = expert_base(ew.gate, ew.table, e, PAIR ? 0 : which, (uint64_t)F, ew.gate_stride);
     const uint8_t *wu = PAIR ? expert_base(ew.up, ew.table, e, 1, (uint64_t)F, ew.up_stride) : wg;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
@@ -96,7 +99,7 @@ k_decode_gate_up_sel(const float *__restrict__ x, int n_used, ExpertWeights ew, 
     const bool certified = !__syncthreads_or(ok ? 0 : 1);   // pooled: the general path needs every wave
     const int e = certified ? __builtin_amdgcn_readlane(e_rank, kk)
                             : cert_select_tokens<1>(x, K, cs.w, cs.wstride, cs.ca, ra, t, emit, sel_prod)[kk];
-    gate_up_rows<GT, G, UPL, true>(x + (int64_t)t * K, slot, e, ew, K, F, 0, h);
+    gate_up_rows<GT, G, UPL, true, DS3_SEL_RPW>(x + (int64_t)t * K, slot, e, ew, K, F, 0, h);
     if (certified && emit && wave == 0) cert_emit_any(cs.ca, ra, t, lane, e_rank);
 }
 
@@ -212,7 +215,7 @@ hipError_t launch_decode_gate_up_sel(const float *x, int T, int n_used, const Ex
         ra.k != n_used || ra.idx == nullptr || ra.scores == nullptr || !router_cert_ok(K, ra.E, n_used))
         return hipErrorInvalidValue;
     const int G = lanes_per_row(K / 32), UPL = K / 32 / G;
-    const int rows_per_wg = (DEC_TPB / WAVE) * (WAVE / G) * 2;
+    const int rows_per_wg = (DEC_TPB / WAVE) * (WAVE / G) * DS3_SEL_RPW;
     const dim3 grid((unsigned)((F + rows_per_wg - 1) / rows_per_wg), (unsigned)(T * n_used));
     const size_t lds = (size_t)cs.ca.nb * (K + 4) * sizeof(float);
     DS3_T_SWITCH(ew.gate_type, DS3_G_SWITCH(G, DS3_U_SWITCH(UPL, hipLaunchKernelGGL(

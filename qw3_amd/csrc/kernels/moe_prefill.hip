@@ -45,18 +45,6 @@ constexpr int N_XCD = 8;                  // MI355X: workgroups go round-robin t
 
 #define DS3_LDS __attribute__((address_space(3)))
 
-template <int TYPE>
-__device__ __forceinline__ int slot_k0(int s, int g, int q)
-{
-    const int c = g + 4 * (q >> 2), part = q & 3;
-    if constexpr (TYPE == T_Q4_K)
-        return 256 * s + 64 * (c >> 1) + 16 * (c & 1) + 8 * (part & 1) + 32 * (part >> 1);
-    else if constexpr (TYPE == T_Q6_K)
-        return 256 * s + 128 * (c >> 2) + 32 * part + 8 * (c & 3);
-    else
-        return 256 * s + 32 * c + 8 * part;
-}
-
 __device__ __forceinline__ const uint8_t *ebase(const uint8_t *base, const uint64_t *table, int e, int which,
                                                 uint64_t rows, uint64_t stride)
 {

@@ -38,18 +38,29 @@ __device__ __forceinline__ float readlane_f(float v, int l)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
-// Softmax + top-k + renorm of one token by one wave (wv < 4: its LDS slot)
-// from its E logits at lg; writes the k indices to oi and weights to os.  The
-// pointers may address global memory or LDS.
-__device__ inline void route_token_row(const float *lg, int E, int k, bool norm, int32_t *oi, float *os, int wv,
-                                       int lane)
+// Wavefront max of unsigned values (lanes without a source read 0).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
 {
-    const uint64_t below = (1ull << lane) - 1ull;
-    __shared__ int cand_s[4][WAVE];
-    __shared__ float val_s[4][WAVE];
-    __shared__ float ord_v_s[4][WAVE];
-    __shared__ int ord_e_s[4][WAVE];
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
 
+// Inverse of order_key.
+__device__ __forceinline__ float key_float(uint32_t k)
+{
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// Softmax + top-k + renorm of one token by one wave from its E logits at lg
+// (E <= 256); writes the k indices to oi and weights to os.  The pointers
+// may address global memory or LDS.
+__device__ inline void route_token_row(const float *lg, int E, int k, bool norm, int32_t *oi, float *os, int lane)
+{
     float l[ROUTE_EPL];
     bool finite = true;
 #pragma unroll
@@ -60,78 +71,70 @@ __device__ inline void route_token_row(const float *lg, int E, int k, bool norm,
     }
     const bool all_finite = __all(finite);
 
-    const int need = min(k + 1, E);
-
-    // Fast path: the need = min(k+1, E) largest logits by a radix select on
-    // order keys (ballot counts, no shuffles), ranked by (value desc, index
-    // asc).  A gap above 2^-19 between neighbours keeps their probabilities
-    // at least 16 ulp apart, so expf cannot tie or reorder them: the logit
-    // order is then the reference's (prob desc) order.
+    // Fast path, in registers: k rounds of a wavefront max over 32-bit keys
+    // (the logit's order key with its low 8 bits replaced by 255 - e, so each
+    // round's winner is unique and carries its index).  The truncation can
+    // only misorder logits within 256 ulps of each other, so the result is
+    // accepted only if every gap is above 2^-19: between neighbours in the
+    // top k (a misordered pair shows a negative gap somewhere between them),
+    // and between the k-th and the largest logit not taken (full keys).  Such
+    // gaps keep the probabilities at least 16 ulp apart, so expf cannot tie
+    // or reorder them: the logit order is then the reference's (prob desc)
+    // order.
     if (all_finite) {
-        uint32_t key[ROUTE_EPL];
-#pragma unroll
-        for (int j = 0; j < ROUTE_EPL; j++) key[j] = lane + WAVE * j < E ? order_key(l[j]) : 0u;
-        uint32_t thr = 0u;                      // largest key with >= need keys at or above it
-        for (int bit = 31; bit >= 0; bit--) {
-            const uint32_t tr = thr | (1u << bit);
-            int cnt = 0;
-#pragma unroll
-            for (int j = 0; j < ROUTE_EPL; j++) cnt += __popcll(__ballot(key[j] >= tr));
-            if (cnt >= need) thr = tr;
-        }
-        int S = 0;
+        uint32_t key[ROUTE_EPL], full[ROUTE_EPL];
 #pragma unroll
         for (int j = 0; j < ROUTE_EPL; j++) {
-            const bool in = key[j] >= thr;
-            const uint64_t m = __ballot(in);
-            const int pos = S + __popcll(m & below);
-            if (in && pos < WAVE) {
-                cand_s[wv][pos] = lane + WAVE * j;
-                val_s[wv][pos] = l[j];
-            }
-            S += __popcll(m);
+            const int e = lane + WAVE * j;
+            full[j] = e < E ? order_key(l[j]) : 0u;             // finite logits: >= 2^23
+            key[j] = e < E ? (full[j] & 0xffffff00u) | (uint32_t)(255 - e) : 0u;
         }
-        if (S <= WAVE) {                        // else: a tie wider than a wave, general path
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            float vi = 0.f;
-            int ei = 0, rank = 0;
-            if (lane < S) {
-                vi = val_s[wv][lane];
-                ei = cand_s[wv][lane];
-                for (int c = 0; c < S; c++) {
-                    const float vc = val_s[wv][c];
-                    rank += (vc > vi || (vc == vi && cand_s[wv][c] < ei)) ? 1 : 0;
-                }
-            }
-            if (lane < S) {
-                ord_v_s[wv][rank] = vi;
-                ord_e_s[wv][rank] = ei;
-            }
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            const float my_v = lane < need ? ord_v_s[wv][lane] : 0.f;
-            const int my_e = lane < need ? ord_e_s[wv][lane] : 0;
-            const float prev_v = (lane >= 1 && lane < need) ? ord_v_s[wv][lane - 1] : 0.f;
-            const bool ok = lane == 0 || lane >= need || prev_v - my_v > 0x1.0p-19f;
-            if (__all(ok)) {
-                const float mx = ord_v_s[wv][0];
-                float sp = 0.f;
+        int my_e = 0;
+        float my_v = 0.f, prev_v = 0.f;
+        for (int r = 0; r < k; r++) {
+            uint32_t m = key[0];
 #pragma unroll
-                for (int j = 0; j < ROUTE_EPL; j++)
-                    if (lane + WAVE * j < E) sp += expf(l[j] - mx);
-                const float inv = 1.0f / wave_sum(sp);
-                const float p = expf(my_v - mx) * inv;
-                float ssum = 0.f;
-                for (int r = 0; r < k; r++) ssum += readlane_f(p, r);     // sequential, in k order
-                if (lane < k) {
-                    float w = p;
-                    if (norm && ssum > 0.0f) w *= 1.0f / ssum;
-                    oi[lane] = my_e;
-                    os[lane] = w;
+            for (int j = 1; j < ROUTE_EPL; j++) m = max(m, key[j]);
+            m = wave_max_u32(m);
+            const int e = 255 - (int)(m & 255u);
+            float v = 0.f;
+#pragma unroll
+            for (int j = 0; j < ROUTE_EPL; j++)
+                if (j == (e >> 6)) v = readlane_f(l[j], e & (WAVE - 1));
+            my_e = lane == r ? e : my_e;
+            my_v = lane == r ? v : my_v;
+            prev_v = lane == r + 1 ? v : prev_v;
+#pragma unroll
+            for (int j = 0; j < ROUTE_EPL; j++)
+                if (lane + WAVE * j == e) {
+                    key[j] = 0u;
+                    full[j] = 0u;
                 }
-                return;                         // uniform over the wave
+        }
+        uint32_t rk = full[0];
+#pragma unroll
+        for (int j = 1; j < ROUTE_EPL; j++) rk = max(rk, full[j]);
+        rk = wave_max_u32(rk);                                  // 0: no logit left
+        bool ok = true;
+        if (lane >= 1 && lane < k) ok = prev_v - my_v > 0x1.0p-19f;
+        if (lane == k - 1 && rk != 0u) ok = ok && my_v - key_float(rk) > 0x1.0p-19f;
+        if (__all(ok)) {
+            const float mx = readlane_f(my_v, 0);
+            float sp = 0.f;
+#pragma unroll
+            for (int j = 0; j < ROUTE_EPL; j++)
+                if (lane + WAVE * j < E) sp += expf(l[j] - mx);
+            const float inv = 1.0f / wave_sum(sp);
+            const float p = expf(my_v - mx) * inv;
+            float ssum = 0.f;
+            for (int r = 0; r < k; r++) ssum += readlane_f(p, r);     // sequential, in k order
+            if (lane < k) {
+                float w = p;
+                if (norm && ssum > 0.0f) w *= 1.0f / ssum;
+                oi[lane] = my_e;
+                os[lane] = w;
             }
+            return;                             // uniform over the wave
         }
     }
 
@@ -184,10 +187,10 @@ __device__ inline void route_token_row(const float *lg, int E, int k, bool norm,
 }
 
 // Softmax + top-k + renorm of token t of a by one wave.
-__device__ inline void route_token(const RouteArgs &a, int t, int wv, int lane)
+__device__ inline void route_token(const RouteArgs &a, int t, int lane)
 {
     route_token_row(a.logits + (int64_t)t * a.logit_stride, a.E, a.k, a.norm, a.idx + (int64_t)t * a.out_stride,
-                    a.scores + (int64_t)t * a.out_stride, wv, lane);
+                    a.scores + (int64_t)t * a.out_stride, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -431,18 +434,6 @@ __device__ __forceinline__ double wave_max_dpp_d(double v)
     v = fmax(v, dpp_do<0x142, 0xa>(v, -INFINITY));
     v = fmax(v, dpp_do<0x143, 0xc>(v, -INFINITY));
     return readlane_d(v, 63);
-}
-
-// Wavefront max of unsigned values (lanes without a source read 0).
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
-{
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));
-    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 // Outputs of a certified token t from its ranking (lane r < k: expert
@@ -746,7 +737,7 @@ __device__ inline const int *cert_select_tokens(const float *__restrict__ x, int
     if (any) {
         if (wave < TG && fail_s[wave]) {
             const int t = t0 + wave;
-            route_token_row(lg_s[wave], E, k, a.norm, ord_s[wave], wt_s[wave], wave, lane);
+            route_token_row(lg_s[wave], E, k, a.norm, ord_s[wave], wt_s[wave], lane);
             if (emit) {
                 __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
                 __builtin_amdgcn_wave_barrier();

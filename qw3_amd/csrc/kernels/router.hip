@@ -470,7 +470,7 @@ k_router_small(const float *__restrict__ x, int T, int K, int E, const float *__
         __syncthreads();
         if (last_s) {
             __threadfence();
-            for (int tt = t0 + wave; tt < min(t0 + 4, T); tt += 3) route_token(topk, tt, wave, lane);
+            for (int tt = t0 + wave; tt < min(t0 + 4, T); tt += 3) route_token(topk, tt, lane);
             if (tid == 0) tickets[blockIdx.x] = 0;
         }
     }
@@ -481,7 +481,7 @@ __global__ void __launch_bounds__(256) k_route(RouteArgs a)
     const int lane = threadIdx.x & (WAVE - 1);
     const int t = blockIdx.x * (blockDim.x / WAVE) + threadIdx.x / WAVE;
     if (t >= a.T) return;                      // whole wave leaves together
-    route_token(a, t, threadIdx.x / WAVE, lane);
+    route_token(a, t, lane);
 }
 
 // ---------------------------------------------------------------------------
