@@ -18,6 +18,9 @@ __device__ __forceinline__ const uint8_t *expert_base(const uint8_t *base, const
 }
 
 constexpr int DEC_TPB = 256;
+#ifndef DS3_DOWN_LDS
+#define DS3_DOWN_LDS 1         // Q6_K down rows staged through LDS by DMA
+#endif
 #ifndef DS3_SEL_RPW
 #define DS3_SEL_RPW 2          // rows per lane group in the fused-selection gate/up kernel
 #endif
@@ -144,6 +147,114 @@ k_decode_down(const float *__restrict__ h, const int32_t *__restrict__ idx, cons
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q6_K down with the weights staged through LDS.  Same work split and the
+// same arithmetic as k_decode_down<Q6_K, 8, UPL> (so the same results, bit
+// for bit): wave k of the workgroup is slot k, lane group (8 lanes) per row,
+// 8 rows per wave, UPL = F / 256 units per lane.  The wave's 8 rows are
+// contiguous (8 x 210 UPL bytes, a multiple of 16) and arrive by 16-byte
+// global_load_lds DMAs together with the slot's h row, so a lane's unit
+// fields (8-byte runs at 2-byte offsets: three dword reads and two funnel
+// shifts each) and its h come from LDS instead of ~40 small global loads.
+// N % 8 == 0, F % 256 == 0 with F <= 1024, rows packed (stride 210 UPL),
+// 16-byte aligned expert bases and h.
+// ---------------------------------------------------------------------------
+#define DS3_LDSP __attribute__((address_space(3)))
+
+__device__ __forceinline__ uint2 lds_u64_a2(uint32_t a)
+{
+    const DS3_LDSP uint32_t *q = (const DS3_LDSP uint32_t *)(uintptr_t)(a & ~3u);
+    const uint32_t sh = a & 3u;
+    const uint32_t w0 = q[0], w1 = q[1], w2 = q[2];
+    return make_uint2(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh));
+}
+
+// unit_dot_q6k with the row's block and x in LDS (byte addresses)
+__device__ __forceinline__ float unit_dot_q6k_lds(uint32_t row, int u, uint32_t xa)
+{
+    const int b = u >> 3, h = (u >> 2) & 1, j = u & 3;
+    const uint32_t blk = row + (uint32_t)b * 210u;
+    const uint2 lo = lds_u64_a2(blk + 64 * h + 8 * j);
+    const uint2 hi = lds_u64_a2(blk + 64 * h + 32 + 8 * j);
+    const uint2 qh = lds_u64_a2(blk + 128 + 32 * h + 8 * j);
+    const uint2 scw = lds_u64_a2(blk + 192 + 8 * h);       // scales[8h .. 8h+7]
+    const float d = h2f(*(const DS3_LDSP uint16_t *)(uintptr_t)(blk + 208));
+    const int s0 = j >> 1;                                  // group (8j)/16 within the half
+    const DS3_LDSP float *xb = (const DS3_LDSP float *)(uintptr_t)xa + 256 * b + 128 * h + 8 * j;
+    const uint32_t low[2] = { lo.x, lo.y }, hig[2] = { hi.x, hi.y }, hb[2] = { qh.x, qh.y };
+    float acc = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const uint32_t sc_byte = byte_of(t < 2 ? scw.x : scw.y, (s0 + 2 * t) & 3);
+        const float sc = (float)(int8_t)sc_byte;
+        const DS3_LDSP float *xt = xb + 32 * t;
+        float dc = 0.f, sx = 0.f;
+#pragma unroll
+        for (int w = 0; w < 2; w++) {
+            const uint32_t ql = (t & 1) ? hig[w] : low[w];
+            const uint32_t nib = (t < 2) ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
+            const uint32_t two = (hb[w] >> (2 * t)) & 0x03030303u;
+            const uint32_t code = nib | (two << 4);          // 0..63 per byte
+            dc += dot4(code, xt + 4 * w);
+            sx += sum4(xt + 4 * w);
+        }
+        acc += sc * (dc - 32.f * sx);
+    }
+    return d * acc;
+}
+
+template <int UPL>
+__global__ void __launch_bounds__(1024)
+k_decode_down_q6k(const float *__restrict__ h, const int32_t *__restrict__ idx, const float *__restrict__ wts,
+                  int n_used, ExpertWeights ew, int N, int F, float *__restrict__ out, int64_t ldo,
+                  const float *__restrict__ residual, int accumulate)
+{
+    constexpr int G = 8, RPW = WAVE / G, ROWB = 210 * UPL;
+    constexpr int WB = RPW * ROWB, REGION = WB + 1024 * UPL;   // 8 rows, then h (F = 256 UPL floats)
+    extern __shared__ __attribute__((aligned(16))) uint8_t dsm[];
+    const int t = blockIdx.y;
+    const int k = threadIdx.x / WAVE;          // one wave per selected expert
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int slot = t * n_used + k;
+    const int e = idx[slot];
+    const int j0 = blockIdx.x * RPW;
+    const uint8_t *src = expert_base(ew.down, ew.table, e, 2, (uint64_t)N, ew.down_stride) + (size_t)j0 * ROWB;
+    const float *hs = h + (int64_t)slot * F;
+    const uint32_t reg = (uint32_t)(uintptr_t)(DS3_LDSP void *)dsm + (uint32_t)(k * REGION);
+    // rows: WB / 16 chunks, 64 per instruction (the last one partly masked); h: 64 UPL chunks
+#pragma unroll
+    for (int i = 0; i < (WB / 16 + WAVE - 1) / WAVE; i++) {
+        const int c = WAVE * i + lane;
+        if (c < WB / 16)
+            __builtin_amdgcn_global_load_lds(src + 16 * c, (DS3_LDSP void *)(uintptr_t)(reg + 1024u * i), 16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < UPL; i++)
+        __builtin_amdgcn_global_load_lds(hs + 256 * i + 4 * lane, (DS3_LDSP void *)(uintptr_t)(reg + WB + 1024u * i),
+                                         16, 0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's rows and h are in LDS (its own region)
+    const int gl = lane % G, grp = lane / G;
+    const uint32_t row = reg + (uint32_t)(grp * ROWB);
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < UPL; i++) acc += unit_dot_q6k_lds(row, gl + G * i, reg + WB);
+    acc = group_sum<G>(acc);
+    float *part = (float *)(dsm + n_used * REGION);        // [n_used][RPW]
+    if (gl == 0) part[k * RPW + grp] = acc;
+    __syncthreads();
+    for (int rr = threadIdx.x; rr < RPW; rr += blockDim.x) {
+        const int jj = j0 + rr;
+        float *o = out + (int64_t)t * ldo + jj;
+        {
+#pragma clang fp contract(off)
+            float a = accumulate ? *o : 0.0f;
+            for (int kk = 0; kk < n_used; kk++) a = a + wts[t * n_used + kk] * part[kk * RPW + rr];
+            if (residual) a = a + residual[(int64_t)t * ldo + jj];
+            *o = a;
+        }
+    }
+}
+
 // Lanes per row: the largest power of two <= 64 dividing the row's units.
 static int lanes_per_row(int units)
 {
@@ -235,6 +346,20 @@ hipError_t launch_decode_down(const float *h, const int32_t *idx, const float *w
 {
     if (!gemv_type_ok(ew.down_type, F) || T <= 0 || N <= 0 || n_used <= 0 || n_used > 16)
         return hipErrorInvalidValue;
+    if (DS3_DOWN_LDS && ew.down_type == T_Q6_K && N % 8 == 0 && F % 256 == 0 && F <= 1024 &&
+        ew.down_stride == (uint64_t)(210 * (F / 256)) && ((uintptr_t)ew.down & 15) == 0 &&
+        (ew.table == nullptr) && ((uintptr_t)h & 15) == 0) {
+        const int upl = F / 256;
+        const size_t lds = (size_t)n_used * (8 * 210 * upl + 1024 * upl) + (size_t)n_used * 8 * sizeof(float);
+        const dim3 grid((unsigned)(N / 8), (unsigned)T);
+        if (lds <= 163840) switch (upl) {
+        case 1: hipLaunchKernelGGL(k_decode_down_q6k<1>, grid, dim3(n_used * WAVE), lds, s, h, idx, wts, n_used, ew, N, F, out, ldo, residual, accumulate ? 1 : 0); break;
+        case 2: hipLaunchKernelGGL(k_decode_down_q6k<2>, grid, dim3(n_used * WAVE), lds, s, h, idx, wts, n_used, ew, N, F, out, ldo, residual, accumulate ? 1 : 0); break;
+        case 3: hipLaunchKernelGGL(k_decode_down_q6k<3>, grid, dim3(n_used * WAVE), lds, s, h, idx, wts, n_used, ew, N, F, out, ldo, residual, accumulate ? 1 : 0); break;
+        default: hipLaunchKernelGGL(k_decode_down_q6k<4>, grid, dim3(n_used * WAVE), lds, s, h, idx, wts, n_used, ew, N, F, out, ldo, residual, accumulate ? 1 : 0); break;
+        }
+        if (lds <= 163840) return hipGetLastError();
+    }
     const int G = lanes_per_row(F / 32), UPL = F / 32 / G;
     const int rpw = WAVE / G;                   // one row per lane group
     const dim3 grid((unsigned)((N + rpw - 1) / rpw), (unsigned)T);
