@@ -21,23 +21,36 @@ namespace ds3k {
 constexpr int BUCKET_TPB = 1024;
 constexpr size_t BUCKET_LDS_BYTES = 60 * 1024;   // masks (u32) + prefix (u16)
 
-// Exclusive prefix sums of (a, b) over the workgroup's threads in thread
-// order; totals returned in ta, tb.
-__device__ __forceinline__ void block_scan2(int &a, int &b, int &ta, int &tb, int2 *wsum)
+// Inclusive prefix sum over the wavefront (DPP row shifts, then rows 1 and 3
+// add lane 15 of the row below, rows 2 and 3 lane 31).
+__device__ __forceinline__ int wave_scan_i(int v)
+{
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);
+    return v;
+}
+
+// Exclusive prefix sums of (a, b) over threads 0 .. n-1 (the first waves of
+// the workgroup; every thread calls it); totals returned in ta, tb.
+__device__ __forceinline__ void block_scan2(int &a, int &b, int &ta, int &tb, int n, int2 *wsum)
 {
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
-    int ia = a, ib = b;
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-        const int ua = __shfl_up(ia, o, WAVE), ub = __shfl_up(ib, o, WAVE);
-        if (lane >= o) { ia += ua; ib += ub; }
+    const int nw = (n + WAVE - 1) / WAVE;
+    int ia = 0, ib = 0;
+    if (wave < nw) {
+        ia = wave_scan_i(a);
+        ib = wave_scan_i(b);
+        if (lane == WAVE - 1) wsum[wave] = make_int2(ia, ib);
     }
-    if (lane == WAVE - 1) wsum[wave] = make_int2(ia, ib);
     __syncthreads();
     int pa = 0, pb = 0;
     ta = 0;
     tb = 0;
-    for (int w = 0; w < BUCKET_TPB / WAVE; w++) {
+    for (int w = 0; w < nw; w++) {
         const int2 v = wsum[w];
         if (w < wave) { pa += v.x; pb += v.y; }
         ta += v.x;
@@ -46,6 +59,8 @@ __device__ __forceinline__ void block_scan2(int &a, int &b, int &ta, int &tb, in
     a = pa + ia - a;
     b = pb + ib - b;
 }
+
+constexpr int BUCKET_CACHE = 8;          // slots per thread kept in registers between the passes
 
 __global__ void __launch_bounds__(BUCKET_TPB)
 k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int T, int k, int E, BucketOut o)
@@ -57,12 +72,24 @@ k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int 
     __shared__ int32_t off_s[BUCKET_TPB];
     __shared__ int2 wsum[BUCKET_TPB / WAVE];
     const int S = T * k;
+    int ex_c[BUCKET_CACHE];
+    float sc_c[BUCKET_CACHE];
+#pragma unroll
+    for (int i = 0; i < BUCKET_CACHE; i++) {             // the slots' ids and scores, loaded once
+        const int s = threadIdx.x + BUCKET_TPB * i;
+        ex_c[i] = s < S ? idx[s] : -1;
+        sc_c[i] = s < S ? scores[s] : 0.f;
+    }
     for (int i = threadIdx.x; i < chunks * E; i += BUCKET_TPB) mask[i] = 0u;
     __syncthreads();
-    for (int s = threadIdx.x; s < S; s += BUCKET_TPB) {
-        const int t = s / k, e = idx[s];
+    auto mark = [&](int s, int e) {
+        const int t = s / k;
         if (e >= 0 && e < E) atomicOr(&mask[(t >> 5) * E + e], 1u << (t & 31));
-    }
+    };
+#pragma unroll
+    for (int i = 0; i < BUCKET_CACHE; i++)
+        if (threadIdx.x + BUCKET_TPB * i < S) mark(threadIdx.x + BUCKET_TPB * i, ex_c[i]);
+    for (int s = threadIdx.x + BUCKET_TPB * BUCKET_CACHE; s < S; s += BUCKET_TPB) mark(s, idx[s]);
     __syncthreads();
     // thread e: its expert's per-chunk prefix, count and work items
     const int e = threadIdx.x;                            // E <= BUCKET_TPB
@@ -75,7 +102,7 @@ k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int 
     }
     int off = cnt, tb = (cnt + o.tile_m - 1) / o.tile_m, total = 0, total_t = 0;
     const int ntile = tb;
-    block_scan2(off, tb, total, total_t, wsum);
+    block_scan2(off, tb, total, total_t, E, wsum);
     if (e < E) {
         o.counts[e] = cnt;
         o.offsets[e] = off;
@@ -87,19 +114,23 @@ k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int 
         *o.n_tiles = total_t < o.max_tiles ? total_t : o.max_tiles;
     }
     __syncthreads();
-    for (int s = threadIdx.x; s < S; s += BUCKET_TPB) {
-        const int t = s / k, ex = idx[s];
+    auto place = [&](int s, int ex, float sc) {
+        const int t = s / k;
         if (ex < 0 || ex >= E) {          // out-of-range id: the slot is dropped
             o.slot_pos[s] = -1;
-            continue;
+            return;
         }
         const int w = (t >> 5) * E + ex;
         const int rank = (int)pre[w] + __popc(mask[w] & ((1u << (t & 31)) - 1u));
         const int pos = off_s[ex] + rank;
         o.ids[pos] = t;
-        o.wts[pos] = scores[s];
+        o.wts[pos] = sc;
         o.slot_pos[s] = pos;
-    }
+    };
+#pragma unroll
+    for (int i = 0; i < BUCKET_CACHE; i++)
+        if (threadIdx.x + BUCKET_TPB * i < S) place(threadIdx.x + BUCKET_TPB * i, ex_c[i], sc_c[i]);
+    for (int s = threadIdx.x + BUCKET_TPB * BUCKET_CACHE; s < S; s += BUCKET_TPB) place(s, idx[s], scores[s]);
 }
 
 hipError_t launch_bucket(const int32_t *idx, const float *scores, int T, int k, int E, const BucketOut &o,
