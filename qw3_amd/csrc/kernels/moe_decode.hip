@@ -18,6 +18,10 @@ __device__ __forceinline__ const uint8_t *expert_base(const uint8_t *base, const
 }
 
 constexpr int DEC_TPB = 256;
+#ifndef DS3_DOWN_PREFETCH
+#define DS3_DOWN_PREFETCH 1    // T = 1: the fused gate/up kernel warms L2 with the down rows
+#endif
+constexpr int N_XCD_DEC = 8;   // MI355X: workgroups go round-robin to 8 XCDs
 #ifndef DS3_DOWN_LDS
 #define DS3_DOWN_LDS 1         // Q6_K down rows staged through LDS by DMA
 #endif
@@ -102,8 +106,31 @@ k_decode_gate_up_sel(const float *__restrict__ x, int n_used, ExpertWeights ew, 
     const bool certified = !__syncthreads_or(ok ? 0 : 1);   // pooled: the general path needs every wave
     const int e = certified ? __builtin_amdgcn_readlane(e_rank, kk)
                             : cert_select_tokens<1>(x, K, cs.w, cs.wstride, cs.ca, ra, t, emit, sel_prod)[kk];
+    // Warm each XCD's L2 with the down rows its down workgroups will read:
+    // workgroups go round-robin to the 8 XCDs in dispatch order, so down
+    // workgroup x (rows 8x .. 8x+7 of every selected expert, one token) runs
+    // on XCD x % 8, as does this workgroup's linear index.  One dword per
+    // 64-byte line; the values are only consumed, never stored.
+    uint32_t pf = 0u;
+    // (whole 16-byte aligned 8-row blocks: every dword read lies inside them)
+    if (DS3_DOWN_PREFETCH && certified && n_used <= WAVE && K % 8 == 0 && ew.table == nullptr &&
+        (8 * ew.down_stride) % 16 == 0 && ((uintptr_t)ew.down & 15) == 0) {
+        const int nx = gridDim.x, lin = blockIdx.y * nx + blockIdx.x, nwg = nx * gridDim.y;
+        const int xcd = lin % N_XCD_DEC, li = lin / N_XCD_DEC, nli = (nwg - xcd + N_XCD_DEC - 1) / N_XCD_DEC;
+        const int K_rows = K, dwg = K_rows / 8;                // down: n_embd rows, 8 per workgroup
+        const int pairs = (dwg - xcd + N_XCD_DEC - 1) / N_XCD_DEC * n_used;
+        const int lines = (int)((8 * ew.down_stride + 63) / 64);
+        for (int p = li; p < pairs; p += nli) {
+            const int xd = xcd + N_XCD_DEC * (p / n_used), k = p - (p / n_used) * n_used;
+            const int ek = __builtin_amdgcn_readlane(e_rank, k);
+            const uint8_t *base = expert_base(ew.down, ew.table, ek, 2, (uint64_t)K_rows, ew.down_stride) +
+                                  (size_t)8 * xd * ew.down_stride;
+            for (int l = threadIdx.x; l < lines; l += DEC_TPB) pf ^= *(const uint32_t *)(base + 64 * (size_t)l);
+        }
+    }
     gate_up_rows<GT, G, UPL, true, DS3_SEL_RPW>(x + (int64_t)t * K, slot, e, ew, K, F, 0, h);
     if (certified && emit && wave == 0) cert_emit_any(cs.ca, ra, t, lane, e_rank);
+    asm volatile("" ::"v"(pf));                // the prefetch loads stay
 }
 
 // One wave per selected expert k, lane group (G lanes) per output row, UPL
