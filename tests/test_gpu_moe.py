@@ -419,6 +419,27 @@ def test_decode_near_ties_fused_select(hip_ready, real, T):
         assert_close(o1.read(np.float32, (1, 2048)), want, rel_l2=5e-5)
 
 
+@pytest.mark.parametrize("n_embd,n_ff,n_expert,n_used", [
+    (1024, 256, 32, 4),       # one Q6_K superblock per down row
+    (1024, 512, 32, 8),
+    (2048, 1024, 32, 8),      # four superblocks per down row, 87 KiB of staged rows per workgroup
+    (1024, 1024, 32, 16),     # 16 slots would need 173 KiB of LDS: the unstaged down kernel
+])
+def test_decode_down_shapes(hip_ready, n_embd, n_ff, n_expert, n_used):
+    """Decode (T = 1 fused selection + L2 warm-up, T = 3 separate selection)
+    on Q4_K gate/up and Q6_K down of other widths and slot counts than
+    Qwen3's, through the staged and unstaged down kernels."""
+    spec = W.LayerSpec(n_embd=n_embd, n_ff=n_ff, n_expert=n_expert)
+    case = Case(spec, seed=500 + n_ff + n_used)
+    for T in (1, 3):
+        x = W.fill(W.NORMAL, 7, T, T * n_embd, 0.0, 1.0).reshape(T, n_embd)
+        want, oi, _, probs = case.oracle(x, n_used=n_used)
+        print(f"  decode {n_embd}x{n_ff} E={n_expert} k={n_used} T={T}", flush=True)
+        got, gi, _, _ = case.gpu_batch(x, n_used=n_used)
+        assert index_mismatches(gi, oi, probs) == 0
+        assert_close(got, want, rel_l2=5e-5)
+
+
 def test_decode_stack_teacher_forced_config4(hip_ready):
     """Configuration 4 in small: h <- h + MoE_l(h) through distinct layers at
     T = 1 (decode path, residual fused), each layer checked against the
