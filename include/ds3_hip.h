@@ -122,6 +122,14 @@ int ds3_hip_scatter_add_weighted_f32(const ds3_hip_buffer_t *src, const ds3_hip_
 int ds3_hip_silu_mul_f32(const ds3_hip_buffer_t *gate, const ds3_hip_buffer_t *up, ds3_hip_buffer_t *out,
                          uint32_t n);
 
+/* reference src/ds3_metal.h:48-57 (the FFN block's prologue, src/ds3_engine.c:522):
+ * out[r] = x[r] / sqrt(mean(x[r]^2) + eps) * weight for n_rows rows of n.
+ * The reference's formula; the sum of squares is a fixed-order tree, so the
+ * result can differ from the CPU reference's left-to-right sum in the last
+ * bits (as the reference's own Metal kernel's does). */
+int ds3_hip_rms_norm(const ds3_hip_buffer_t *x, const ds3_hip_buffer_t *weight, ds3_hip_buffer_t *out,
+                     uint32_t n, uint32_t n_rows, float eps);
+
 /* ---------------------------------------------------------------------- */
 /* MoE FFN                                                                */
 /* ---------------------------------------------------------------------- */
@@ -211,6 +219,23 @@ int ds3_hip_moe_ffn_batch(
     uint64_t gate_row_stride, uint64_t up_row_stride, uint64_t down_row_stride,
     const ds3_hip_buffer_t *expert_offsets,
     ds3_hip_buffer_t *output, const ds3_hip_buffer_t *residual,
+    ds3_hip_buffer_t *gate_logits, ds3_hip_buffer_t *indices, ds3_hip_buffer_t *scores,
+    uint32_t n_tokens, uint32_t n_embd, uint32_t n_expert, uint32_t n_used, uint32_t n_ff_exp,
+    uint64_t router_row_stride, ds3_hip_type_t router_type, bool norm_topk_prob);
+
+/* The engine's whole FFN block for T tokens in one call (reference
+ * src/ds3_engine.c:519-527 and 675-720: rms_norm, zeroing, moe_ffn and the
+ * residual vec_add): hidden[t] += MoE(rms_norm(hidden[t]) * ffn_norm), in
+ * place.  The normalised rows go to x_norm when given (it must not overlap
+ * hidden), else to the library's workspace; everything else as
+ * ds3_hip_moe_ffn_batch with input = the normalised rows, output = hidden
+ * (accumulating) and no separate residual.  No counterpart in ds3_metal.h. */
+int ds3_hip_moe_block(
+    ds3_hip_buffer_t *hidden, const ds3_hip_buffer_t *ffn_norm, float eps, const ds3_hip_buffer_t *w_gate_inp,
+    const ds3_hip_buffer_t *w_gate_exps, const ds3_hip_buffer_t *w_up_exps, const ds3_hip_buffer_t *w_down_exps,
+    ds3_hip_type_t gate_type, ds3_hip_type_t up_type, ds3_hip_type_t down_type,
+    uint64_t gate_row_stride, uint64_t up_row_stride, uint64_t down_row_stride,
+    const ds3_hip_buffer_t *expert_offsets, ds3_hip_buffer_t *x_norm,
     ds3_hip_buffer_t *gate_logits, ds3_hip_buffer_t *indices, ds3_hip_buffer_t *scores,
     uint32_t n_tokens, uint32_t n_embd, uint32_t n_expert, uint32_t n_used, uint32_t n_ff_exp,
     uint64_t router_row_stride, ds3_hip_type_t router_type, bool norm_topk_prob);

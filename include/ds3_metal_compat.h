@@ -37,6 +37,7 @@ typedef ds3_hip_buffer_t ds3_metal_buffer_t;
 #define ds3_metal_gather_rows_f32 ds3_hip_gather_rows_f32
 #define ds3_metal_scatter_add_weighted_f32 ds3_hip_scatter_add_weighted_f32
 #define ds3_metal_silu_mul_f32 ds3_hip_silu_mul_f32
+#define ds3_metal_rms_norm ds3_hip_rms_norm
 #define ds3_metal_moe_ffn ds3_hip_moe_ffn
 #define ds3_metal_moe_ffn_router ds3_hip_moe_ffn_router
 #define ds3_metal_moe_ffn_experts ds3_hip_moe_ffn_experts

@@ -42,6 +42,7 @@ SIGNATURES: dict[str, tuple] = {
     "ds3_hip_gather_rows_f32": (C.c_int, [P, P, P, U32, U32, U32]),
     "ds3_hip_scatter_add_weighted_f32": (C.c_int, [P, P, P, P, U32, U32, U32]),
     "ds3_hip_silu_mul_f32": (C.c_int, [P, P, P, U32]),
+    "ds3_hip_rms_norm": (C.c_int, [P, P, P, U32, U32, F]),
     "ds3_hip_moe_ffn": (C.c_int, [P, P, P, P, P, I32, I32, I32, U64, U64, U64,
                                   P, P, P, I32, I32, I32, U64, U64, U64,
                                   P, P, P, P, P, P, U32, U32, U32, U32, U32, U64, I32, B]),
@@ -58,6 +59,8 @@ SIGNATURES: dict[str, tuple] = {
     "ds3_hip_profile_print": (None, [CP]),
     "ds3_hip_moe_ffn_batch": (C.c_int, [P, P, P, P, P, I32, I32, I32, U64, U64, U64, P,
                                         P, P, P, P, P, U32, U32, U32, U32, U32, U64, I32, B]),
+    "ds3_hip_moe_block": (C.c_int, [P, P, F, P, P, P, P, I32, I32, I32, U64, U64, U64, P,
+                                    P, P, P, P, U32, U32, U32, U32, U32, U64, I32, B]),
     "ds3_hip_moe_route": (C.c_int, [P, P, P, P, P, U32, U32, U32, U32, U64, I32, B]),
     "ds3_hip_moe_bucket": (C.c_int, [P, P, U32, U32, U32, P, P, P, P, P]),
     "ds3_hip_dequantize": (C.c_int, [P, U64, I32, U64, P]),

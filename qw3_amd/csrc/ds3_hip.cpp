@@ -572,6 +572,18 @@ extern "C" int ds3_hip_silu_mul_f32(const ds3_hip_buffer_t *gate, const ds3_hip_
     return finish(launch_silu_mul(fptr(gate), fptr(up), fptr(out), n, g.stream), "silu_mul_f32");
 }
 
+// reference src/ds3_metal.h:48-57 (metal/rms_norm.metal; CPU src/ds3_reference.c:329-342)
+extern "C" int ds3_hip_rms_norm(const ds3_hip_buffer_t *x, const ds3_hip_buffer_t *weight, ds3_hip_buffer_t *out,
+                                uint32_t n, uint32_t n_rows, float eps)
+{
+    if (!x || !weight || !out || n == 0 || n_rows == 0 || !(eps >= 0.0f) || !ensure_init()) return -1;
+    const size_t bytes = (size_t)n * n_rows * 4;
+    if (!fits(x, bytes, "x") || !fits(weight, (size_t)n * 4, "weight") || !fits(out, bytes, "out")) return -1;
+    KScope ks("rms_norm");
+    return finish(launch_rms_norm(fptr(x), fptr(weight), fptr(out), (int)n, (int)n_rows, eps, n, n, g.stream),
+                  "rms_norm");
+}
+
 // ===========================================================================
 // MoE
 // ===========================================================================
@@ -977,16 +989,29 @@ extern "C" int ds3_hip_moe_bucket(const ds3_hip_buffer_t *indices, const ds3_hip
                   "moe_bucket");
 }
 
-extern "C" int ds3_hip_moe_ffn_batch(
-    const ds3_hip_buffer_t *input, const ds3_hip_buffer_t *w_gate_inp, const ds3_hip_buffer_t *w_gate_exps,
-    const ds3_hip_buffer_t *w_up_exps, const ds3_hip_buffer_t *w_down_exps, ds3_hip_type_t gate_type,
-    ds3_hip_type_t up_type, ds3_hip_type_t down_type, uint64_t gate_row_stride, uint64_t up_row_stride,
-    uint64_t down_row_stride, const ds3_hip_buffer_t *expert_offsets, ds3_hip_buffer_t *output,
-    const ds3_hip_buffer_t *residual, ds3_hip_buffer_t *gate_logits, ds3_hip_buffer_t *indices,
-    ds3_hip_buffer_t *scores, uint32_t n_tokens, uint32_t n_embd, uint32_t n_expert, uint32_t n_used,
-    uint32_t n_ff_exp, uint64_t router_row_stride, ds3_hip_type_t router_type, bool norm_topk_prob)
+namespace {
+
+// Optional RMSNorm prologue of moe_batch: the input rows are the hidden state,
+// and the MoE runs on rms_norm(hidden) * weight, written to xn (or workspace).
+struct NormIn {
+    const float *weight;
+    float eps;
+    float *xn;
+};
+
+// The batch MoE of ds3_hip_moe_ffn_batch / ds3_hip_moe_block on raw device
+// rows: input x_in [T][n_embd]; out (+)= result (+ residual res); the routing
+// outputs (logits, indices, scores) are optional.
+int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_gate_inp,
+              const ds3_hip_buffer_t *w_gate_exps, const ds3_hip_buffer_t *w_up_exps,
+              const ds3_hip_buffer_t *w_down_exps, ds3_hip_type_t gate_type, ds3_hip_type_t up_type,
+              ds3_hip_type_t down_type, uint64_t gate_row_stride, uint64_t up_row_stride, uint64_t down_row_stride,
+              const ds3_hip_buffer_t *expert_offsets, float *out, const float *res, float *logits_out,
+              int32_t *idx_out, float *scores_out, uint32_t n_tokens, uint32_t n_embd, uint32_t n_expert,
+              uint32_t n_used, uint32_t n_ff_exp, uint64_t router_row_stride, ds3_hip_type_t router_type,
+              bool norm_topk_prob, const char *what)
 {
-    if (!input || !w_gate_inp || !w_gate_exps || !w_up_exps || !w_down_exps || !output) return -1;
+    if (!w_gate_inp || !w_gate_exps || !w_up_exps || !w_down_exps) return -1;
     if (n_tokens == 0 || n_embd == 0 || n_expert == 0 || n_used == 0 || n_ff_exp == 0 || n_used > n_expert)
         return -1;
     if (!quant_type_ok_for_moe(gate_type, n_embd, "gate") || !quant_type_ok_for_moe(up_type, n_embd, "up") ||
@@ -998,10 +1023,6 @@ extern "C" int ds3_hip_moe_ffn_batch(
         return -1;
     }
     const size_t T = n_tokens;
-    if (!fits(input, T * n_embd * 4, "input") || !fits(output, T * n_embd * 4, "output") ||
-        !fits(residual, T * n_embd * 4, "residual") || !fits(gate_logits, T * n_expert * 4, "gate_logits") ||
-        !fits(indices, T * n_used * 4, "indices") || !fits(scores, T * n_used * 4, "scores"))
-        return -1;
 
     const bool grouped_ok = gate_type == up_type && grouped_type_ok(gate_type, (int)n_embd) &&
                             grouped_type_ok(down_type, (int)n_ff_exp) && n_ff_exp % 128 == 0 && n_embd % 128 == 0;
@@ -1012,6 +1033,7 @@ extern "C" int ds3_hip_moe_ffn_batch(
     const int max_tiles = (int)((S + 63) / 64) + (int)n_expert;
 
     Bump bp;
+    const size_t o_xn = norm && !norm->xn ? bp.take(T * n_embd * 4) : 0;
     const size_t o_l = bp.take(T * n_expert * 4), o_i = bp.take(T * n_used * 4), o_s = bp.take(T * n_used * 4);
     const RouteScratch rs = route_scratch((int)T, n_embd, n_expert);
     const size_t o_w = bp.take(rs.bytes);
@@ -1034,11 +1056,18 @@ extern "C" int ds3_hip_moe_ffn_batch(
     }
     uint8_t *ws = ws_get(bp.off);
     if (!ws) return -1;
-    const RouteBufs rb = route_bufs(ws + o_w, rs, gate_logits ? fptr(gate_logits) : (float *)(ws + o_l),
-                                    indices ? (int32_t *)dptr(indices) : (int32_t *)(ws + o_i),
-                                    scores ? fptr(scores) : (float *)(ws + o_s),
+    const RouteBufs rb = route_bufs(ws + o_w, rs, logits_out ? logits_out : (float *)(ws + o_l),
+                                    idx_out ? idx_out : (int32_t *)(ws + o_i), scores_out ? scores_out : (float *)(ws + o_s),
                                     use_grouped ? (_Float16 *)(ws + o_x16) : nullptr);
-    const float *x = fptr(input);
+    const float *x = x_in;
+    if (norm) {
+        float *xn = norm->xn ? norm->xn : (float *)(ws + o_xn);
+        KScope ks("rms_norm");
+        const hipError_t e = launch_rms_norm(x_in, norm->weight, xn, (int)n_embd, (int)T, norm->eps, n_embd, n_embd,
+                                             g.stream);
+        if (e != hipSuccess) return report(e, what);
+        x = xn;
+    }
     bool x16_done = false;
     DeferredSel sel;
     if (route_tokens(x, w_gate_inp, router_row_stride, router_type, (int)T, n_embd, n_expert, n_used, norm_topk_prob,
@@ -1046,13 +1075,11 @@ extern "C" int ds3_hip_moe_ffn_batch(
         return -1;
     ExpertWeights ew = make_ew(w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type, down_type, gate_row_stride,
                                up_row_stride, down_row_stride, expert_offsets);
-    float *out = fptr(output);
-    const float *res = residual ? fptr(residual) : nullptr;
     if (!use_grouped) {
         if (run_experts_decode(x, n_embd, rb.idx, rb.scores, (int)T, (int)n_used, ew, n_embd, n_ff_exp, out, res, true,
                                (float *)(ws + o_h), (float *)(ws + o_t), &sel) != 0)
             return -1;
-        return finish(hipSuccess, "moe_ffn_batch");
+        return finish(hipSuccess, what);
     }
     BucketOut bo{ (int32_t *)(ws + o_cnt), (int32_t *)(ws + o_off), (int32_t *)(ws + o_ids), (float *)(ws + o_wts),
                   (int32_t *)(ws + o_pos), (int32_t *)(ws + o_tiles), (int32_t *)(ws + o_nt), max_tiles, 64 };
@@ -1061,7 +1088,7 @@ extern "C" int ds3_hip_moe_ffn_batch(
     if (!x16_done) {
         KScope ks("to_f16");
         const hipError_t e = launch_to_f16(x, x16_all, (int64_t)T * n_embd, g.stream);
-        if (e != hipSuccess) return report(e, "moe_ffn_batch to_f16");
+        if (e != hipSuccess) return report(e, what);
     }
     for (size_t t0 = 0; t0 < T; t0 += Tc) {
         const int tc = (int)((T - t0) < Tc ? (T - t0) : Tc);
@@ -1085,9 +1112,61 @@ extern "C" int ds3_hip_moe_ffn_batch(
             e = launch_combine(y, bo.slot_pos, rb.scores + t0 * n_used, tc, (int)n_used, (int)n_embd,
                                out + t0 * n_embd, n_embd, res ? res + t0 * n_embd : nullptr, true, g.stream);
         }
-        if (e != hipSuccess) return report(e, "moe_ffn_batch grouped");
+        if (e != hipSuccess) return report(e, what);
     }
-    return finish(hipSuccess, "moe_ffn_batch");
+    return finish(hipSuccess, what);
+}
+
+}  // namespace
+
+extern "C" int ds3_hip_moe_ffn_batch(
+    const ds3_hip_buffer_t *input, const ds3_hip_buffer_t *w_gate_inp, const ds3_hip_buffer_t *w_gate_exps,
+    const ds3_hip_buffer_t *w_up_exps, const ds3_hip_buffer_t *w_down_exps, ds3_hip_type_t gate_type,
+    ds3_hip_type_t up_type, ds3_hip_type_t down_type, uint64_t gate_row_stride, uint64_t up_row_stride,
+    uint64_t down_row_stride, const ds3_hip_buffer_t *expert_offsets, ds3_hip_buffer_t *output,
+    const ds3_hip_buffer_t *residual, ds3_hip_buffer_t *gate_logits, ds3_hip_buffer_t *indices,
+    ds3_hip_buffer_t *scores, uint32_t n_tokens, uint32_t n_embd, uint32_t n_expert, uint32_t n_used,
+    uint32_t n_ff_exp, uint64_t router_row_stride, ds3_hip_type_t router_type, bool norm_topk_prob)
+{
+    if (!input || !output) return -1;
+    const size_t T = n_tokens;
+    if (!fits(input, T * n_embd * 4, "input") || !fits(output, T * n_embd * 4, "output") ||
+        !fits(residual, T * n_embd * 4, "residual") || !fits(gate_logits, T * n_expert * 4, "gate_logits") ||
+        !fits(indices, T * n_used * 4, "indices") || !fits(scores, T * n_used * 4, "scores"))
+        return -1;
+    return moe_batch(fptr(input), nullptr, w_gate_inp, w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type,
+                     down_type, gate_row_stride, up_row_stride, down_row_stride, expert_offsets, fptr(output),
+                     residual ? fptr(residual) : nullptr, gate_logits ? fptr(gate_logits) : nullptr,
+                     indices ? (int32_t *)dptr(indices) : nullptr, scores ? fptr(scores) : nullptr, n_tokens, n_embd,
+                     n_expert, n_used, n_ff_exp, router_row_stride, router_type, norm_topk_prob, "moe_ffn_batch");
+}
+
+// reference src/ds3_engine.c:519-527, 675-720 (rms_norm, zero, moe_ffn, vec_add around the MoE)
+extern "C" int ds3_hip_moe_block(
+    ds3_hip_buffer_t *hidden, const ds3_hip_buffer_t *ffn_norm, float eps, const ds3_hip_buffer_t *w_gate_inp,
+    const ds3_hip_buffer_t *w_gate_exps, const ds3_hip_buffer_t *w_up_exps, const ds3_hip_buffer_t *w_down_exps,
+    ds3_hip_type_t gate_type, ds3_hip_type_t up_type, ds3_hip_type_t down_type, uint64_t gate_row_stride,
+    uint64_t up_row_stride, uint64_t down_row_stride, const ds3_hip_buffer_t *expert_offsets,
+    ds3_hip_buffer_t *x_norm, ds3_hip_buffer_t *gate_logits, ds3_hip_buffer_t *indices, ds3_hip_buffer_t *scores,
+    uint32_t n_tokens, uint32_t n_embd, uint32_t n_expert, uint32_t n_used, uint32_t n_ff_exp,
+    uint64_t router_row_stride, ds3_hip_type_t router_type, bool norm_topk_prob)
+{
+    if (!hidden || !ffn_norm || !(eps >= 0.0f)) return -1;
+    const size_t T = n_tokens;
+    if (!fits(hidden, T * n_embd * 4, "hidden") || !fits(ffn_norm, (size_t)n_embd * 4, "ffn_norm") ||
+        !fits(x_norm, T * n_embd * 4, "x_norm") || !fits(gate_logits, T * n_expert * 4, "gate_logits") ||
+        !fits(indices, T * n_used * 4, "indices") || !fits(scores, T * n_used * 4, "scores"))
+        return -1;
+    if (x_norm) {                                                     // the normalised rows must not overlap hidden
+        const uint8_t *a = cptr(x_norm), *h = cptr(hidden);
+        if (a < h + T * n_embd * 4 && h < a + T * n_embd * 4) return -1;
+    }
+    const NormIn norm{ fptr(ffn_norm), eps, x_norm ? fptr(x_norm) : nullptr };
+    return moe_batch(fptr(hidden), &norm, w_gate_inp, w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type,
+                     down_type, gate_row_stride, up_row_stride, down_row_stride, expert_offsets, fptr(hidden), nullptr,
+                     gate_logits ? fptr(gate_logits) : nullptr, indices ? (int32_t *)dptr(indices) : nullptr,
+                     scores ? fptr(scores) : nullptr, n_tokens, n_embd, n_expert, n_used, n_ff_exp, router_row_stride,
+                     router_type, norm_topk_prob, "moe_block");
 }
 
 extern "C" int ds3_hip_dequantize(const ds3_hip_buffer_t *src, uint64_t src_offset, ds3_hip_type_t type, uint64_t n,

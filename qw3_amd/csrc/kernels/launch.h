@@ -142,6 +142,11 @@ hipError_t launch_combine(const float *y, const int32_t *slot_pos, const float *
                           int N, float *out, int64_t ldo, const float *residual, bool accumulate,
                           hipStream_t s);
 
+// RMSNorm of n_rows rows of n floats (row strides ldx, ldo):
+// out = x * (1 / sqrt(mean(x^2) + eps)) * w (reference src/ds3_reference.c:329-342).
+hipError_t launch_rms_norm(const float *x, const float *w, float *out, int n, int n_rows, float eps, int64_t ldx,
+                           int64_t ldo, hipStream_t s);
+
 // Elementwise helpers (reference metal/elementwise.metal, metal/moe.metal:95-127).
 hipError_t launch_fill_zero(float *p, int64_t n, hipStream_t s);
 hipError_t launch_copy(const float *a, float *b, int64_t n, hipStream_t s);

@@ -151,6 +151,25 @@ def moe_ffn_batch(x: Buffer, router: Buffer, router_type: int, ex: ExpertTensors
         "moe_ffn_batch")
 
 
+def moe_block(hidden: Buffer, ffn_norm: Buffer, eps: float, router: Buffer, router_type: int, ex: ExpertTensors,
+              n_tokens: int, n_expert: int, n_used: int, x_norm: Buffer | None = None, logits: Buffer | None = None,
+              indices: Buffer | None = None, scores: Buffer | None = None, norm: bool = True,
+              expert_offsets: Buffer | None = None) -> None:
+    """The engine's FFN block in place: hidden += MoE(rms_norm(hidden) * ffn_norm)."""
+    gs, us, ds = ex.strides
+    _check(hip().ds3_hip_moe_block(
+        hidden, ffn_norm, eps, router, ex.gate, ex.up, ex.down,
+        ex.gate_type, ex.up_type, ex.down_type, gs, us, ds, _h(expert_offsets),
+        _h(x_norm), _h(logits), _h(indices), _h(scores),
+        n_tokens, ex.n_embd, n_expert, n_used, ex.n_ff, row_bytes(router_type, ex.n_embd), router_type, norm),
+        "moe_block")
+
+
+def rms_norm(x: Buffer, weight: Buffer, out: Buffer, n: int, n_rows: int, eps: float) -> None:
+    """ds3_metal_rms_norm-compatible (reference src/ds3_metal.h:48-57)."""
+    _check(hip().ds3_hip_rms_norm(x, weight, out, n, n_rows, eps), "rms_norm")
+
+
 def moe_ffn(x: Buffer, router: Buffer, router_type: int, ex: ExpertTensors, out: Buffer, logits: Buffer,
             n_expert: int, n_used: int, norm: bool = True, scratch: Buffer | None = None,
             shared: ExpertTensors | None = None, n_ff_shared: int = 0, expert_offsets: Buffer | None = None) -> None:

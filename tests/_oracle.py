@@ -112,6 +112,16 @@ def ref_dequantize(type_: int, raw: np.ndarray, n: int) -> np.ndarray:
     return out
 
 
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """Rows of x normalised as src/ds3_reference.c:329-342 does (left-to-right sum of squares)."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    for r in range(x.shape[0]):
+        orc().orc_rms_norm(ptr(x[r]), ptr(w), eps, x.shape[1], ptr(out[r]))
+    return out
+
+
 def vec_matmul(x: np.ndarray, W: np.ndarray) -> np.ndarray:
     out_dim, in_dim = W.shape
     y = np.empty(out_dim, np.float32)
