@@ -48,6 +48,8 @@ def parse():
     p.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
                    help="2, 3, 5: one layer on --tokens tokens (+ T=1 under t1); 4: the decode stack")
     p.add_argument("--stack-layers", type=int, default=48, help="config 4: resident layers per decode step")
+    p.add_argument("--stack-block", action="store_true",
+                   help="config 4: run each layer as the engine's FFN block (RMSNorm + MoE + residual)")
     p.add_argument("--t1-steps", type=int, default=200)
     p.add_argument("--no-t1", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
@@ -209,9 +211,11 @@ def cpu_baseline(layer, x, n_used, n_tokens):
 
 def run_stack(args, n_used=8):
     """Configuration 4: one token per step through a resident stack of
-    --stack-layers MoE layers, h <- h + MoE_l(h) (output zeroed, then the
-    residual fused into the call), as the engine runs decode.  Returns the
-    JSON line."""
+    --stack-layers MoE layers, h <- h + MoE_l(h) in place (the call
+    accumulates into its own input), as the engine runs decode.  With
+    --stack-block each layer is the engine's whole FFN block instead,
+    h <- h + MoE_l(rms_norm(h) * g_l) (ds3_hip_moe_block).  Returns the JSON
+    line."""
     from qw3_amd import ds3
     from qw3_amd import workload as W
     from qw3_amd._native import hip
@@ -222,17 +226,19 @@ def run_stack(args, n_used=8):
     log(f"[bench] config 4: {L} layers generated and resident in {time.perf_counter() - t0:.1f}s "
         f"({L * (W.expert_bytes(spec) * E + W.router_bytes(spec)) / 2**30:.2f} GiB)")
     hs = [ds3.Buffer.from_array(W.make_inputs(4, 1, seed=99, step=s)) for s in range(8)]
-    bufs = [ds3.Buffer.alloc(K * 4) for _ in range(2)]
+    h = ds3.Buffer.alloc(K * 4)
     idx = ds3.Buffer.alloc(n_used * 4)
+    gains = [ds3.Buffer.from_array((1.0 + W.fill(W.NORMAL, 700 + l, 1, K, 0.0, 0.02)).astype(np.float32))
+             for l in range(L)] if args.stack_block else None
 
     def token(i, want_idx=False):
-        src = hs[i % len(hs)]
+        hip().ds3_hip_buffer_copy_f32(hs[i % len(hs)], h, K * 4)     # a fresh hidden state, on the device
         for l, d in enumerate(layers):
-            dst = bufs[l & 1]
-            dst.zero()
-            ds3.moe_ffn_batch(src, d.router, spec.router_type, d.experts, dst, 1, E, n_used, residual=src,
-                              indices=idx if (want_idx and l == 0) else None)
-            src = dst
+            ix = idx if (want_idx and l == 0) else None
+            if gains is not None:
+                ds3.moe_block(h, gains[l], 1e-6, d.router, spec.router_type, d.experts, 1, E, n_used, indices=ix)
+            else:
+                ds3.moe_ffn_batch(h, d.router, spec.router_type, d.experts, h, 1, E, n_used, indices=ix)
 
     token(0, want_idx=True)
     hip().ds3_hip_synchronize()
@@ -281,7 +287,9 @@ def run_stack(args, n_used=8):
         "dtype": "f16",
         "data": "synthetic (seeded generator; expert weights N(0,0.02) quantised by this project's GGUF quantisers)",
         "config": {"workload": f"configs[3]: decode, one token through {L} resident Qwen3-30B-A3B MoE-FFN layers, "
-                               f"h <- h + MoE_l(h); Q4_K gate/up + Q6_K down, F32 router",
+                               + ("h <- h + MoE_l(rms_norm(h) * g_l) (the engine's FFN block); " if args.stack_block
+                                  else "h <- h + MoE_l(h); ")
+                               + "Q4_K gate/up + Q6_K down, F32 router",
                    "tokens": 1, "layers": L, "n_embd": K, "n_ff": spec.n_ff},
         "roofline": roofline(stats, spec, 1, counts, n_used, traffic),
         "alg_bytes_per_step": b,

@@ -204,7 +204,8 @@ void ds3_hip_profile_print(const char *label);
  * fp16-MFMA products + in-order combine.  Replaces the engine's decode and
  * gathered-prefill sequences (reference src/ds3_engine.c:520-597, 895-1022).
  *   input [T][n_embd] f32; output [T][n_embd] f32 accumulates (caller
- *   zeroes); residual (optional) [T][n_embd] is added to output;
+ *   zeroes); residual (optional) [T][n_embd] is added to output; output
+ *   may be input itself (input += MoE(input), in place, no residual);
  *   indices / scores (optional) receive the routing [T][n_used];
  *   gate_logits (optional) receives the logits [T][n_expert].
  * Up to 16 tokens (see ds3_hip_set_router_mode) the router is the certified

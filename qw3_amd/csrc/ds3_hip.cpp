@@ -674,10 +674,12 @@ bool use_cert(const float *x, int T, uint32_t n_embd, uint32_t n_expert, uint32_
 // Router logits + softmax/top-k/renorm for T tokens.  Sets *x16_done when the
 // router also wrote rb.x16.  With defer, a certified selection may be left to
 // the decode gate/up kernel (defer->on): the routing outputs are then written
-// by that kernel.
+// by that kernel.  With np (certified router only), x holds raw rows and the
+// router's sums kernel normalises them, writing np->xn, which the rest of the
+// routing reads.
 int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstride, int rtype, int T, uint32_t n_embd,
                  uint32_t n_expert, uint32_t n_used, bool norm, const RouteBufs &rb, bool *x16_done = nullptr,
-                 bool allow_cert = false, DeferredSel *defer = nullptr)
+                 bool allow_cert = false, DeferredSel *defer = nullptr, const NormPro *np = nullptr)
 {
     RouteArgs ra{};
     ra.logits = rb.logits;
@@ -694,8 +696,9 @@ int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstrid
         {
             KScope ks("router_sums");
             e = launch_router_cert(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, rb.wf32,
-                                   rb.logits, n_expert, rb.x16, ra, rb.cert, g.cert_stats, 1, g.stream);
+                                   rb.logits, n_expert, rb.x16, ra, rb.cert, g.cert_stats, 1, g.stream, np);
         }
+        if (np != nullptr) x = np->xn;
         if (e == hipSuccess && defer != nullptr && T <= kFuseSelMaxTokens) {
             // repair batch of the fused kernel: 4 candidate rows (~32 KiB of
             // LDS at K = 2048) keep 3 of its workgroups per CU at T <= 2
@@ -715,6 +718,7 @@ int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstrid
         if (x16_done) *x16_done = rb.x16 != nullptr;
         return report(e, "router (certified)");
     }
+    if (np != nullptr) return report(hipErrorInvalidValue, "router: fused norm needs the certified router");
     bool topk_done = false;
     {
         KScope ks("router_logits");
@@ -1059,20 +1063,31 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
     const RouteBufs rb = route_bufs(ws + o_w, rs, logits_out ? logits_out : (float *)(ws + o_l),
                                     idx_out ? idx_out : (int32_t *)(ws + o_i), scores_out ? scores_out : (float *)(ws + o_s),
                                     use_grouped ? (_Float16 *)(ws + o_x16) : nullptr);
+    // The norm: fused into the certified router's sums kernel where that
+    // router serves the call, else its own launch before the router.
     const float *x = x_in;
+    NormPro np{};
+    bool fuse_norm = false;
     if (norm) {
         float *xn = norm->xn ? norm->xn : (float *)(ws + o_xn);
-        KScope ks("rms_norm");
-        const hipError_t e = launch_rms_norm(x_in, norm->weight, xn, (int)n_embd, (int)T, norm->eps, n_embd, n_embd,
-                                             g.stream);
-        if (e != hipSuccess) return report(e, what);
-        x = xn;
+        np = NormPro{ norm->weight, norm->eps, xn };
+        fuse_norm = use_cert(x_in, (int)T, n_embd, n_expert, n_used, true) &&
+                    ((uintptr_t)norm->weight & 15) == 0 && ((uintptr_t)xn & 15) == 0;
+        if (!fuse_norm) {
+            KScope ks("rms_norm");
+            const hipError_t e = launch_rms_norm(x_in, norm->weight, xn, (int)n_embd, (int)T, norm->eps, n_embd,
+                                                 n_embd, g.stream);
+            if (e != hipSuccess) return report(e, what);
+            x = xn;
+        }
     }
     bool x16_done = false;
     DeferredSel sel;
     if (route_tokens(x, w_gate_inp, router_row_stride, router_type, (int)T, n_embd, n_expert, n_used, norm_topk_prob,
-                     rb, &x16_done, true, !use_grouped && gate_type == up_type ? &sel : nullptr) != 0)
+                     rb, &x16_done, true, !use_grouped && gate_type == up_type ? &sel : nullptr,
+                     fuse_norm ? &np : nullptr) != 0)
         return -1;
+    if (fuse_norm) x = np.xn;
     ExpertWeights ew = make_ew(w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type, down_type, gate_row_stride,
                                up_row_stride, down_row_stride, expert_offsets);
     if (!use_grouped) {

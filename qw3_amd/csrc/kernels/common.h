@@ -682,6 +682,19 @@ __device__ __forceinline__ float group_sum(float v)
 
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<WAVE>(v); }
 
+// RMSNorm's reduction order, shared by k_rms_norm and the certified router's
+// fused prologue so both produce the same bits: in a 256-thread workgroup,
+// thread t sums the squares of its contiguous run of ceil(n / 256) elements in
+// index order, wave_sum adds the 64 lane partials, and the four wave totals are
+// added in wave order; the scale is 1 / sqrt(ss / n + eps).
+constexpr int NORM_THREADS = 256;
+__device__ __forceinline__ float norm_rms(const float (&part)[4], int n, float eps)
+{
+#pragma clang fp contract(off)
+    const float ss = ((part[0] + part[1]) + part[2]) + part[3];
+    return 1.0f / sqrtf(ss / (float)n + eps);
+}
+
 __device__ __forceinline__ float wave_max(float v)
 {
 #pragma unroll

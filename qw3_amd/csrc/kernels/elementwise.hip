@@ -115,37 +115,39 @@ __global__ void k_combine(const float *__restrict__ y, const int32_t *__restrict
 // RMSNorm of one row per workgroup (reference src/ds3_reference.c:329-342,
 // metal/rms_norm.metal): out = x * (1 / sqrt(mean(x^2) + eps)) * weight, with
 // the reference's formula (sum / n, + eps, 1 / sqrtf, then (x * rms) * w).
-// The sum of squares is a fixed-order tree (strided per-thread partial sums,
-// a wavefront butterfly, the four wave totals in order), not the reference's
-// left-to-right chain, so rms can differ from it in the last bits, as the
-// reference's Metal kernel's does; the result is the same on every call.
-__global__ void __launch_bounds__(256)
+// The sum of squares is a fixed-order tree (norm_rms: per-thread contiguous
+// runs, a wavefront butterfly, the four wave totals in order), not the
+// reference's left-to-right chain, so rms can differ from it in the last bits,
+// as the reference's Metal kernel's does; the result is the same on every call
+// and the same as the certified router's fused prologue.
+__global__ void __launch_bounds__(NORM_THREADS)
 k_rms_norm(const float *__restrict__ x, const float *__restrict__ w, float *__restrict__ out, int n, float eps,
            int64_t ldx, int64_t ldo)
 {
 #pragma clang fp contract(off)
-    __shared__ float part[4];
+    __shared__ float part[NORM_THREADS / WAVE];
     const int64_t row = blockIdx.x;
     const float *xr = x + row * ldx;
+    const int run = (n + NORM_THREADS - 1) / NORM_THREADS;
+    const int b = threadIdx.x * run, e = min(b + run, n);
     float s = 0.f;
-    for (int i = threadIdx.x; i < n; i += 256) {
+    for (int i = b; i < e; i++) {
         const float v = xr[i];
         s = s + v * v;
     }
     s = wave_sum(s);
     if ((threadIdx.x & (WAVE - 1)) == 0) part[threadIdx.x / WAVE] = s;
     __syncthreads();
-    const float ss = ((part[0] + part[1]) + part[2]) + part[3];
-    const float rms = 1.0f / sqrtf(ss / (float)n + eps);
+    const float rms = norm_rms(part, n, eps);
     float *orow = out + row * ldo;
-    for (int i = threadIdx.x; i < n; i += 256) orow[i] = xr[i] * rms * w[i];
+    for (int i = threadIdx.x; i < n; i += NORM_THREADS) orow[i] = xr[i] * rms * w[i];
 }
 
 hipError_t launch_rms_norm(const float *x, const float *w, float *out, int n, int n_rows, float eps, int64_t ldx,
                            int64_t ldo, hipStream_t s)
 {
     if (n <= 0 || n_rows <= 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned)n_rows), dim3(256), 0, s, x, w, out, n, eps, ldx, ldo);
+    hipLaunchKernelGGL(k_rms_norm, dim3((unsigned)n_rows), dim3(NORM_THREADS), 0, s, x, w, out, n, eps, ldx, ldo);
     return hipGetLastError();
 }
 

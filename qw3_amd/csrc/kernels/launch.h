@@ -67,11 +67,22 @@ hipError_t launch_router_seq(const float *x, int T, int K, int E, int rtype, con
 // stats (optional): device counters {tokens certified, tokens repaired}.
 // phases: bit 0 enqueues the sums (after the FP32 row copy of a non-F32
 // router), bit 1 the selection; the same arguments go to both.
+// norm (optional, phase 1 only with it): x holds raw rows and the sums run on
+// rms_norm(x) * norm->w, the values launch_rms_norm computes, bit for bit;
+// the expert-0 workgroups write them to norm->xn [T][K], which the selection
+// phase (and a fused selection) then reads in place of x.  norm->w and
+// norm->xn 16-byte aligned.
+struct NormPro {
+    const float *w;
+    float eps;
+    float *xn;
+};
 bool router_cert_ok(int K, int E, int k);
 size_t router_cert_scratch(int T, int E);
 hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, const uint8_t *rw, uint64_t rstride,
                               float *wf32, float *logits, int64_t ldl, _Float16 *x16, const RouteArgs &ra,
-                              void *scratch, unsigned long long *stats, int phases, hipStream_t s);
+                              void *scratch, unsigned long long *stats, int phases, hipStream_t s,
+                              const NormPro *norm = nullptr);
 
 // What the certified router's selection reads, for a kernel that selects in
 // its own prologue (launch_decode_gate_up_sel) after launch_router_cert's

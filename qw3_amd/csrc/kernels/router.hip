@@ -489,13 +489,16 @@ __global__ void __launch_bounds__(256) k_route(RouteArgs a)
 // ---------------------------------------------------------------------------
 
 // S, B and fl32(S) for TG tokens x one expert.  Lane l of wave w covers
-// elements (64 w + l) L .. + L - 1, K = 256 L.
-template <int L, int TG>
+// elements (64 w + l) L .. + L - 1, K = 256 L.  With NORM the rows are first
+// normalised in RMSNorm's reduction order (norm_rms: the same runs, butterfly
+// and wave order), so every workgroup derives the same xn as k_rms_norm.
+template <int L, int TG, bool NORM>
 __global__ void __launch_bounds__(RC_THREADS)
 k_router_sums(const float *__restrict__ x, int T, int K, int E, const float *__restrict__ w, int64_t wstride,
-              float *__restrict__ logits, int64_t ldl, _Float16 *__restrict__ x16, CertArgs ca)
+              float *__restrict__ logits, int64_t ldl, _Float16 *__restrict__ x16, CertArgs ca, NormPro np)
 {
 #pragma clang fp contract(off)
+    static_assert(RC_THREADS == NORM_THREADS, "the fused norm needs RMSNorm's thread count");
     __shared__ float tot_s[TG][RC_WAVES];
     __shared__ float am_s[TG][RC_WAVES];
     __shared__ double sum_s[TG][RC_WAVES];
@@ -506,6 +509,35 @@ k_router_sums(const float *__restrict__ x, int T, int K, int E, const float *__r
     load_run<L>(w + (int64_t)e * wstride + k0, wv);
 #pragma unroll
     for (int tt = 0; tt < TG; tt++) load_run<L>(x + (int64_t)min(t0 + tt, T - 1) * K + k0, pv[tt]);
+    if constexpr (NORM) {
+        float gv[L];
+        load_run<L>(np.w + k0, gv);
+#pragma unroll
+        for (int tt = 0; tt < TG; tt++) {
+            float q = 0.0f;
+#pragma unroll
+            for (int i = 0; i < L; i++) q = q + pv[tt][i] * pv[tt][i];
+            q = wave_sum(q);
+            if (lane == 0) am_s[tt][wave] = q;      // reused below, after a barrier
+        }
+        __syncthreads();
+#pragma unroll
+        for (int tt = 0; tt < TG; tt++) {
+            const float rms = norm_rms(am_s[tt], K, np.eps);
+#pragma unroll
+            for (int i = 0; i < L; i++) pv[tt][i] = pv[tt][i] * rms * gv[i];
+        }
+        if (blockIdx.y == 0) {
+#pragma unroll
+            for (int tt = 0; tt < TG; tt++) {
+                if (t0 + tt >= T) continue;
+                float *d = np.xn + (int64_t)(t0 + tt) * K + k0;
+#pragma unroll
+                for (int i = 0; i < L; i++) d[i] = pv[tt][i];
+            }
+        }
+        __syncthreads();                            // am_s is rewritten below
+    }
     if (x16 != nullptr && blockIdx.y == 0) {
 #pragma unroll
         for (int tt = 0; tt < TG; tt++) {
@@ -621,11 +653,15 @@ size_t router_cert_scratch(int T, int E) { return (size_t)T * E * (sizeof(double
 
 template <int L, int TG>
 static void cert_sums(const float *x, int T, int K, int E, const float *w, int64_t wstride, float *logits,
-                      int64_t ldl, _Float16 *x16, const CertArgs &ca, hipStream_t s)
+                      int64_t ldl, _Float16 *x16, const CertArgs &ca, const NormPro *np, hipStream_t s)
 {
     const dim3 grid((unsigned)((T + TG - 1) / TG), (unsigned)E);
-    hipLaunchKernelGGL((k_router_sums<L, TG>), grid, dim3(RC_THREADS), 0, s, x, T, K, E, w, wstride, logits, ldl, x16,
-                       ca);
+    if (np != nullptr)
+        hipLaunchKernelGGL((k_router_sums<L, TG, true>), grid, dim3(RC_THREADS), 0, s, x, T, K, E, w, wstride, logits,
+                           ldl, x16, ca, *np);
+    else
+        hipLaunchKernelGGL((k_router_sums<L, TG, false>), grid, dim3(RC_THREADS), 0, s, x, T, K, E, w, wstride,
+                           logits, ldl, x16, ca, NormPro{});
 }
 
 template <int TG>
@@ -657,11 +693,16 @@ hipError_t router_cert_sel(int T, int K, int E, int k, int rtype, const uint8_t 
 
 hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, const uint8_t *rw, uint64_t rstride,
                               float *wf32, float *logits, int64_t ldl, _Float16 *x16, const RouteArgs &ra,
-                              void *scratch, unsigned long long *stats, int phases, hipStream_t s)
+                              void *scratch, unsigned long long *stats, int phases, hipStream_t s,
+                              const NormPro *norm)
 {
     if (ra.logits != logits || ra.logit_stride != ldl || ra.T != T || ra.E != E || ra.idx == nullptr)
         return hipErrorInvalidValue;
     if (((uintptr_t)x & 15) != 0 || ((uintptr_t)x16 & 15) != 0) return hipErrorInvalidValue;
+    if (norm != nullptr &&
+        (phases != 1 || norm->w == nullptr || norm->xn == nullptr || ((uintptr_t)norm->w & 15) != 0 ||
+         ((uintptr_t)norm->xn & 15) != 0 || !(norm->eps >= 0.0f)))
+        return hipErrorInvalidValue;
     // repair batch: up to 13 candidate rows (about 104 KiB of LDS) while one
     // token group is routed, up to 4 (~32 KiB) when several workgroups share CUs
     const int rowb = (K + 4) * (int)sizeof(float);
@@ -685,9 +726,9 @@ hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, co
     const int TG = T == 1 ? 1 : T == 2 ? 2 : 4;
 #define DS3_CERT_SUMS(LV)                                                                        \
     do {                                                                                         \
-        if (TG == 1) cert_sums<LV, 1>(x, T, K, E, w, wstride, logits, ldl, x16, ca, s);          \
-        else if (TG == 2) cert_sums<LV, 2>(x, T, K, E, w, wstride, logits, ldl, x16, ca, s);     \
-        else cert_sums<LV, 4>(x, T, K, E, w, wstride, logits, ldl, x16, ca, s);                  \
+        if (TG == 1) cert_sums<LV, 1>(x, T, K, E, w, wstride, logits, ldl, x16, ca, norm, s);          \
+        else if (TG == 2) cert_sums<LV, 2>(x, T, K, E, w, wstride, logits, ldl, x16, ca, norm, s);     \
+        else cert_sums<LV, 4>(x, T, K, E, w, wstride, logits, ldl, x16, ca, norm, s);                  \
     } while (0)
     if (phases & 1) switch (K / 256) {
     case 1: DS3_CERT_SUMS(1); break;

@@ -668,6 +668,19 @@ def test_rms_norm_entry_point(hip_ready):
     check_norm_ulps(got, x, w, eps, want)
 
 
+@pytest.mark.parametrize("n,rows", [(64, 3), (300, 2), (2048, 5), (4000, 2)])
+def test_rms_norm_shapes(hip_ready, n, rows):
+    """Row lengths that are not a multiple of the 256-thread workgroup (runs of
+    ceil(n / 256) elements per thread, the last threads idle), each row in a
+    workgroup of its own; same bounds as above."""
+    x = W.fill(W.NORMAL, 40 + n, rows, rows * n, 0.0, 1.0).reshape(rows, n)
+    w = (1.0 + W.fill(W.NORMAL, 41 + n, 1, n, 0.0, 0.02)).astype(np.float32)
+    out = ds3.Buffer.alloc(rows * n * 4)
+    print(f"  rms_norm n={n} rows={rows}", flush=True)
+    ds3.rms_norm(ds3.Buffer.from_array(x), ds3.Buffer.from_array(w), out, n, rows, 1e-6)
+    check_norm_ulps(out.read(np.float32, (rows, n)), x, w, 1e-6, O.rms_norm(x, w, 1e-6))
+
+
 def check_norm_ulps(got: np.ndarray, x: np.ndarray, w: np.ndarray, eps: float, want: np.ndarray):
     """got within 8 ulp of the formula in float64 (the tree sum of squares
     rounds about log2(n) times) and within 64 ulp of the reference's result,
@@ -682,14 +695,16 @@ def check_norm_ulps(got: np.ndarray, x: np.ndarray, w: np.ndarray, eps: float, w
     assert u_ref.max() <= 64
 
 
-@pytest.mark.parametrize("T", [1, 3, 64])
+@pytest.mark.parametrize("T", [1, 2, 3, 16, 64])
 def test_moe_block(hip_ready, real, T):
     """hidden += MoE(rms_norm(hidden) * g) in place (reference engine
     src/ds3_engine.c:519-527, 675-720), on the decode (T = 1 fused selection,
-    T = 3) and grouped (T = 64) paths.  The normalised rows (x_norm output)
-    are checked as rms_norm's are; the MoE is checked against
-    the oracle run on those rows (indices exact, outputs to the decode or
-    grouped bar), and a second call without x_norm gives the same hidden."""
+    T = 2, 3, 16) and grouped (T = 64) paths.  Up to 16 tokens the certified
+    router's sums kernel normalises the rows itself; its x_norm must equal
+    the rms_norm entry point's bit for bit, and is checked as rms_norm's is.
+    The MoE is checked against the oracle run on those rows (indices exact,
+    outputs to the decode or grouped bar), and a second call without x_norm
+    gives the same hidden."""
     s = real.spec
     hid = W.fill(W.NORMAL, 31, T, T * s.n_embd, 0.0, 1.0).reshape(T, s.n_embd)
     g = (1.0 + W.fill(W.NORMAL, 32, 1, s.n_embd, 0.0, 0.02)).astype(np.float32)
@@ -701,6 +716,9 @@ def test_moe_block(hip_ready, real, T):
     ds3.moe_block(hb, gb, eps, real.dev.router, s.router_type, real.dev.experts, T, s.n_expert, W.N_USED,
                   x_norm=xn, indices=idx)
     got_xn = xn.read(np.float32, (T, s.n_embd))
+    sep = ds3.Buffer.alloc(T * s.n_embd * 4)
+    ds3.rms_norm(ds3.Buffer.from_array(hid), gb, sep, s.n_embd, T, eps)
+    assert np.array_equal(got_xn.view(np.uint32), sep.read(np.float32, (T, s.n_embd)).view(np.uint32))
     check_norm_ulps(got_xn, hid, g, eps, O.rms_norm(hid, g, eps))
     want, oi, _, probs = real.oracle(got_xn)
     assert index_mismatches(idx.read(np.int32, (T, W.N_USED)), oi, probs) == 0
@@ -709,3 +727,23 @@ def test_moe_block(hip_ready, real, T):
     hb2 = ds3.Buffer.from_array(hid)
     ds3.moe_block(hb2, gb, eps, real.dev.router, s.router_type, real.dev.experts, T, s.n_expert, W.N_USED)
     assert np.array_equal(hb2.read(np.float32, (T, s.n_embd)), after)
+
+
+@pytest.mark.parametrize("T", [1, 5, 64])
+def test_moe_ffn_batch_in_place(hip_ready, real, T):
+    """output may be the input itself: h += MoE(h) with no zeroed output and
+    no residual gives what output = 0, residual = h gives (the same sums,
+    added to h in another order: within a few fp32 roundings)."""
+    s = real.spec
+    hid = W.fill(W.NORMAL, 51, T, T * s.n_embd, 0.0, 1.0).reshape(T, s.n_embd)
+    print(f"  moe_ffn_batch in place T={T}", flush=True)
+    xb, out = ds3.Buffer.from_array(hid), ds3.Buffer.alloc(T * s.n_embd * 4)
+    out.zero()
+    ds3.moe_ffn_batch(xb, real.dev.router, s.router_type, real.dev.experts, out, T, s.n_expert, W.N_USED,
+                      residual=xb)
+    want = out.read(np.float32, (T, s.n_embd))
+    hb = ds3.Buffer.from_array(hid)
+    ds3.moe_ffn_batch(hb, real.dev.router, s.router_type, real.dev.experts, hb, T, s.n_expert, W.N_USED)
+    got = hb.read(np.float32, (T, s.n_embd))
+    # h + (w_1 y_1 + ...) rounds after each of the 8 adds at |h|'s scale instead of once
+    np.testing.assert_allclose(got, want, rtol=0, atol=8 * float(np.spacing(np.abs(want).max())))
