@@ -405,7 +405,8 @@ k_grouped_gate_up(const _Float16 *__restrict__ x16, int K, ExpertWeights ew, int
     using C = GmCfg<TYPE, 2>;
     __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
     const int n_nt = F / C::TILE_N, runs_per_item = (n_nt + ntb - 1) / ntb;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index as a uniform value keeps wave-derived pointers in SGPRs
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     for (int rr = blockIdx.x; rr < n_runs; rr += gridDim.x) {
         int item, run;
         gm_decode_run(rr, runs_per_item, item, run);
@@ -449,7 +450,8 @@ k_grouped_down(const _Float16 *__restrict__ h16, int F, ExpertWeights ew, int N,
     using C = GmCfg<TYPE, 1>;
     __shared__ __attribute__((aligned(16))) uint8_t smem[C::LDS];
     const int n_nt = N / C::TILE_N, runs_per_item = (n_nt + ntb - 1) / ntb;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wave index as a uniform value keeps wave-derived pointers in SGPRs
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     for (int rr = blockIdx.x; rr < n_runs; rr += gridDim.x) {
         int item, run;
         gm_decode_run(rr, runs_per_item, item, run);
