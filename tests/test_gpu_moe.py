@@ -346,6 +346,36 @@ def test_prefill_T2048_skewed_config3(hip_ready, zipf):
     assert_close(got, want)
 
 
+@pytest.mark.parametrize("T", [17, 37, 1000, 2100])
+def test_prefill_ragged_and_chunked(hip_ready, uniform, T):
+    """Grouped path on token counts that are not multiples of the 16-row MFMA
+    blocks or the 64-token tiles, and past one 2048-token bucketing chunk
+    (T = 2100: a full chunk, then 52 tokens)."""
+    x = W.make_inputs(2, T, seed=110 + T)
+    print(f"  prefill ragged T={T}", flush=True)
+    got, gi, gs, _ = uniform.gpu_batch(x, prefill_min=1)
+    want, oi, osc, probs = uniform.oracle(x)
+    assert index_mismatches(gi, oi, probs) == 0
+    assert_close(got, want)
+
+
+def test_prefill_hot_experts(hip_ready):
+    """Every token routed to the same 8 experts (router rows of the other
+    experts zero, the chosen ones scaled up): 512 tokens give each of them 8
+    64-token work items while 120 experts stay empty."""
+    hot = np.array([3, 17, 40, 41, 77, 90, 100, 127])
+    r = np.zeros((128, 2048), np.float32)
+    r[hot] = np.abs(W.fill(W.NORMAL, 77, 5, 8 * 2048, 0.0, 0.02)).reshape(8, 2048)
+    x = np.abs(W.make_inputs(2, 512, seed=120)).astype(np.float32)   # hot logits ~ +26, the rest 0
+    print("  prefill hot experts T=512", flush=True)
+    case = Case(W.LayerSpec(router_dist=W.UNIFORM), seed=77, router=r)
+    got, gi, gs, _ = case.gpu_batch(x, prefill_min=1)
+    want, oi, osc, probs = case.oracle(x)
+    assert set(np.unique(oi).tolist()) == set(hot.tolist())
+    assert index_mismatches(gi, oi, probs) == 0
+    assert_close(got, want)
+
+
 @pytest.mark.parametrize("T", [1, 4, 16, 64, 256, 1024])
 def test_q8_0_sweep_config5(hip_ready, q80, T):
     x = W.make_inputs(5, T, seed=104 + T)
@@ -517,12 +547,16 @@ def test_expert_offset_table(hip_ready, real):
     tbl = np.array([[e * 768 * gs, e * 768 * us, e * 2048 * dsd] for e in range(128)], np.uint64)
     x = W.make_inputs(2, 48, seed=108)
     want, _, _, _ = real.oracle(x)
-    for pm in (1, 1 << 30):
+    for pm in (1, 1 << 30):                     # grouped MFMA path, then the GEMV path
         T = 48
         out = ds3.Buffer.alloc(T * 2048 * 4)
-        ds3.moe_ffn_batch(ds3.Buffer.from_array(x), real.dev.router, 0, real.dev.experts, out, T, 128, 8,
-                          expert_offsets=ds3.Buffer.from_array(tbl))
-        assert_close(out.read(np.float32, (T, 2048)), want)
+        prev = ds3.set_prefill_min_tokens(pm)
+        try:
+            ds3.moe_ffn_batch(ds3.Buffer.from_array(x), real.dev.router, 0, real.dev.experts, out, T, 128, 8,
+                              expert_offsets=ds3.Buffer.from_array(tbl))
+        finally:
+            ds3.set_prefill_min_tokens(prev)
+        assert_close(out.read(np.float32, (T, 2048)), want, rel_l2=1e-3 if pm == 1 else 5e-5)
 
 
 def test_shared_expert(hip_ready):
