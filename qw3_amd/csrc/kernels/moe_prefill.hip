@@ -40,7 +40,11 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // a native vector: copies stay in registers
 
 constexpr int GM_TILE_M = 64;
-constexpr int GM_ROW = 256 + 8;           // halves per LDS row (16-byte pad)
+// Activation tile rows in LDS: 512 bytes (256 halves) each, 16-byte chunk c
+// of row r at r * 512 + 16 * (c ^ (r & 15)).  The XOR swizzle spreads the 16
+// rows one fragment read touches over the banks with no padding, so one
+// 64-lane DMA fills two whole rows.
+constexpr int GM_ROWB = 512;
 constexpr int N_XCD = 8;                  // MI355X: workgroups go round-robin to 8 XCDs
 
 #define DS3_LDS __attribute__((address_space(3)))
@@ -66,9 +70,9 @@ template <> struct WGeo<T_Q8_0> { static constexpr int BLK = 272, CPR = 18; stat
 // every lane issues every instruction: lanes past the last chunk repeat
 // chunk 0 into the padding.
 // LDS layout of one workgroup (bytes): two activation tiles (64 rows of
-// GM_ROW halves) then two weight stages per wave.  WV = waves per workgroup
+// GM_ROWB bytes) then two weight stages per wave.  WV = waves per workgroup
 // (16 output rows each): 8 where that fits 160 KiB of LDS, else 4.
-constexpr int GM_ATILE = GM_TILE_M * GM_ROW * 2;
+constexpr int GM_ATILE = GM_TILE_M * GM_ROWB;
 constexpr int GM_LDS_MAX = 163840;
 template <int TYPE, int NB> struct GmCfg {
     static constexpr int CPR = WGeo<TYPE>::CPR;
@@ -100,17 +104,18 @@ __device__ __forceinline__ void dma16(const void *src, uint32_t lds)
 
 // A fragment reads for K slots 4*hv + 2*pp + {0, 1}: MB row blocks each,
 // all issued before one wait; the wait names every result so nothing reads
-// them early.  Addresses: rowbase (row m of the tile) + 2*(16*mb*GM_ROW +
-// col).
+// them early.  Lane (g, m) reads row 16*mb + m: rowbase (row m) + the
+// swizzled chunk + 16 * GM_ROWB * mb.
 template <int TYPE, int MB>
-__device__ __forceinline__ void a_frags(uint32_t rowbase, int g, int hv, int pp, half8 (&af)[2][4])
+__device__ __forceinline__ void a_frags(uint32_t rowbase, int g, int m, int hv, int pp, half8 (&af)[2][4])
 {
 #pragma unroll
     for (int p = 0; p < 2; p++) {
-        const uint32_t col = 2u * (uint32_t)slot_k0<TYPE>(0, g, 4 * hv + 2 * pp + p);
+        const uint32_t c = (uint32_t)slot_k0<TYPE>(0, g, 4 * hv + 2 * pp + p) / 8u;
+        const uint32_t a = rowbase + 16u * (c ^ (uint32_t)m);
 #pragma unroll
         for (int mb = 0; mb < MB; mb++)
-            asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(af[p][mb]) : "v"(rowbase + col), "i"(2 * 16 * GM_ROW * mb));
+            asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(af[p][mb]) : "v"(a), "i"(16 * GM_ROWB * mb));
     }
     if constexpr (MB == 1)
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(af[0][0]), "+v"(af[1][0]));
@@ -132,7 +137,7 @@ __device__ __forceinline__ void gm_step(uint32_t as, const RawUnits<TYPE> (&raw)
                                         floatx4 (&acc)[4][NB])
 {
     const int g = lane >> 4, m = lane & 15;
-    const uint32_t rowbase = as + 2u * (uint32_t)(m * GM_ROW);
+    const uint32_t rowbase = as + (uint32_t)(m * GM_ROWB);
 #pragma unroll
     for (int hv = 0; hv < 2; hv++) {
         half8 bq[NB][4];
@@ -141,7 +146,7 @@ __device__ __forceinline__ void gm_step(uint32_t as, const RawUnits<TYPE> (&raw)
 #pragma unroll
         for (int pp = 0; pp < 2; pp++) {
             half8 af[2][4];
-            a_frags<TYPE, MB>(rowbase, g, hv, pp, af);
+            a_frags<TYPE, MB>(rowbase, g, m, hv, pp, af);
 #pragma unroll
             for (int p = 0; p < 2; p++)
 #pragma unroll
@@ -162,7 +167,7 @@ constexpr int GM_MAX_NI = 12;      // weight DMA instructions per stage the run 
 template <int NB>
 struct GmRun {
     const _Float16 *a_src;
-    uint32_t a_row[16];             // element offsets of this wave's activation rows wave + WV*j (WV >= 4)
+    uint32_t a_row[8];              // DMA j: element offset of this lane's source chunk (row pair wave + WV*j)
     const uint8_t *rows[NB];        // this lane's weight row in n tile nt0 (decode side)
     const uint8_t *wave_rows[NB];   // the wave's first weight row in n tile nt0, per column block
     uint32_t dma_off[GM_MAX_NI];    // this lane's chunk of DMA instruction i: row * stride of its row
@@ -174,24 +179,23 @@ struct GmRun {
     bool w_dma;                     // weights stream through the LDS ring (else: read in place)
 };
 
-// Loads of flat step v into buffer v & 1, all by DMA: the activation rows
-// wave + WV*j below 16*MB (rows past the tile's tokens repeat its first row;
-// 32 lanes x 16 bytes per row into a padded LDS row) and this wave's weight
+// Loads of flat step v into buffer v & 1, all by DMA: the activation row
+// pairs wave + WV*j below 8*MB (rows past the tile's tokens repeat its first
+// row; 64 lanes x 16 bytes fill two swizzled rows) and this wave's weight
 // stage.
 template <int TYPE, int NB, int MB>
 __device__ __forceinline__ void gm_issue(const GmRun<NB> &r, int v)
 {
     using C = GmCfg<TYPE, NB>;
-    static_assert(16 * MB / C::WV <= 16 && C::NI <= GM_MAX_NI, "run state arrays too small");
+    static_assert(8 * MB % C::WV == 0 && 8 * MB / C::WV <= 8 && C::NI <= GM_MAX_NI, "run state arrays too small");
     using G = WGeo<TYPE>;
     const int buf = v & 1;
     const int wt = v / r.S, ws = v - wt * r.S;
-    if (r.lane < 32) {
+    {
         const uint32_t at = r.lds + (uint32_t)(buf * GM_ATILE);
 #pragma unroll
-        for (int j = 0; j < 16 * MB / C::WV; j++)
-            dma16(r.a_src + r.a_row[j] + 256 * ws + 8 * r.lane,
-                  at + 2u * (uint32_t)((r.wave + C::WV * j) * GM_ROW));
+        for (int j = 0; j < 8 * MB / C::WV; j++)
+            dma16(r.a_src + r.a_row[j] + 256 * ws, at + (uint32_t)(2 * GM_ROWB * (r.wave + C::WV * j)));
     }
     if (!r.w_dma) return;
     const uint64_t step_off = (uint64_t)wt * r.tstride + (uint64_t)ws * G::BLK;
@@ -417,9 +421,9 @@ k_grouped_gate_up(const _Float16 *__restrict__ x16, int K, ExpertWeights ew, int
         r.wave = wave;
         r.a_src = x16;
 #pragma unroll
-        for (int j = 0; j < 64 / C::WV; j++) {
-            const int row = wave + C::WV * j;
-            r.a_row[j] = (uint32_t)b.ids[it.off + it.m0 + (row < it.mrows ? row : 0)] * (uint32_t)K;
+        for (int j = 0; j < 32 / C::WV; j++) {
+            const int row = 2 * (wave + C::WV * j) + (lane >> 5), chunk = (lane & 31) ^ (row & 15);
+            r.a_row[j] = (uint32_t)b.ids[it.off + it.m0 + (row < it.mrows ? row : 0)] * (uint32_t)K + 8u * chunk;
         }
         r.nt0 = run * ntb;
         const int nnt = min(ntb, n_nt - r.nt0);
@@ -462,9 +466,9 @@ k_grouped_down(const _Float16 *__restrict__ h16, int F, ExpertWeights ew, int N,
         r.wave = wave;
         r.a_src = h16;
 #pragma unroll
-        for (int j = 0; j < 64 / C::WV; j++) {
-            const int row = wave + C::WV * j;
-            r.a_row[j] = (uint32_t)(it.off + it.m0 + (row < it.mrows ? row : 0)) * (uint32_t)F;
+        for (int j = 0; j < 32 / C::WV; j++) {
+            const int row = 2 * (wave + C::WV * j) + (lane >> 5), chunk = (lane & 31) ^ (row & 15);
+            r.a_row[j] = (uint32_t)(it.off + it.m0 + (row < it.mrows ? row : 0)) * (uint32_t)F + 8u * chunk;
         }
         r.nt0 = run * ntb;
         const int nnt = min(ntb, n_nt - r.nt0);
