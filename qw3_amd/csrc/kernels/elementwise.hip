@@ -20,16 +20,15 @@ __global__ void k_fill_zero(float *p, int64_t n)
     if (i < n) p[i] = 0.0f;
 }
 
-// 16-byte stores (p 16-byte aligned): four floats per thread, the tail
-// scalar.
+// 16-byte stores (p 16-byte aligned), grid-stride over float4 units; the
+// last n % 4 floats by thread 0 of workgroup 0.
 __global__ void k_fill_zero4(float *p, int64_t n)
 {
-    const int64_t i = 4 * ((int64_t)blockIdx.x * EW_TPB + threadIdx.x);
-    if (i + 4 <= n) {
-        *(float4 *)(p + i) = make_float4(0.f, 0.f, 0.f, 0.f);
-    } else {
-        for (int64_t j = i; j < n; j++) p[j] = 0.0f;
-    }
+    const int64_t n4 = n / 4, stride = (int64_t)gridDim.x * EW_TPB;
+    for (int64_t i = (int64_t)blockIdx.x * EW_TPB + threadIdx.x; i < n4; i += stride)
+        ((float4 *)p)[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        for (int64_t j = 4 * n4; j < n; j++) p[j] = 0.0f;
 }
 
 __global__ void k_copy(const float *a, float *b, int64_t n)
@@ -165,7 +164,12 @@ hipError_t launch_rms_norm(const float *x, const float *w, float *out, int n, in
 
 hipError_t launch_fill_zero(float *p, int64_t n, hipStream_t s)
 {
-    if (((uintptr_t)p & 15) == 0) hipLaunchKernelGGL(k_fill_zero4, grid1d((n + 3) / 4), dim3(EW_TPB), 0, s, p, n);
+    if (((uintptr_t)p & 15) == 0) {
+        // up to 1024 workgroups, each storing 4 KiB per pass
+        const int64_t wg = (n / 4 + EW_TPB - 1) / EW_TPB;
+        hipLaunchKernelGGL(k_fill_zero4, dim3((unsigned)(wg < 1 ? 1 : wg > 1024 ? 1024 : wg)), dim3(EW_TPB), 0, s, p,
+                           n);
+    }
     else hipLaunchKernelGGL(k_fill_zero, grid1d(n), dim3(EW_TPB), 0, s, p, n);
     return hipGetLastError();
 }
