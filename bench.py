@@ -48,6 +48,8 @@ def parse():
     p.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5),
                    help="2, 3, 5: one layer on --tokens tokens (+ T=1 under t1); 4: the decode stack")
     p.add_argument("--stack-layers", type=int, default=48, help="config 4: resident layers per decode step")
+    p.add_argument("--no-graph", action="store_true",
+                   help="config 4: enqueue every layer eagerly instead of replaying the token's layers as one HIP graph")
     p.add_argument("--stack-block", action="store_true",
                    help="config 4: run each layer as the engine's FFN block (RMSNorm + MoE + residual)")
     p.add_argument("--t1-steps", type=int, default=200)
@@ -91,7 +93,9 @@ def kernel_bytes(name, spec, T, counts, n_used):
 def run_gpu(args, T, steps, warmup, layers, xs, spec, n_used=8):
     """Warmup steps with every kernel timed (per-kernel breakdown, choice of
     the dominant kernel), the timed steps with no per-kernel events, then the
-    same steps again with only the dominant kernel bracketed by events."""
+    same steps again with only the dominant kernel bracketed by events.
+    Steps are enqueued eagerly: a captured graph of one step's 4-7 kernels
+    replays slower than the kernels enqueue (T = 1: 29.4 vs 21.6 us)."""
     from qw3_amd import ds3
     from qw3_amd._native import hip
     E, K = spec.n_expert, spec.n_embd
@@ -254,21 +258,52 @@ def run_stack(args, n_used=8):
     brk = ds3.kernel_stats()
     dominant = max((k for k in brk if kernel_bytes(k, spec, 1, counts, n_used) is not None),
                    key=lambda k: brk[k][1])
+    step = token
+    graph = None
+    if not args.no_graph:
+        # the layers as one HIP graph over h: each token copies its fresh
+        # hidden state into h (eagerly), then replays the graph
+        graph = ds3.Graph()
+        with graph:
+            for l, d in enumerate(layers):
+                if gains is not None:
+                    ds3.moe_block(h, gains[l], 1e-6, d.router, spec.router_type, d.experts, 1, E, n_used)
+                else:
+                    ds3.moe_ffn_batch(h, d.router, spec.router_type, d.experts, h, 1, E, n_used)
+
+        def step(i):
+            hip().ds3_hip_buffer_copy_f32(hs[i % len(hs)], h, K * 4)
+            graph.launch()
+
+        hip().ds3_hip_begin_batch()
+        for i in range(1, args.warmup + 1):
+            step(i)
+        hip().ds3_hip_end_batch()
     hip().ds3_hip_kernel_timing_reset()
     hip().ds3_hip_kernel_timing_only(dominant.encode())
-    hip().ds3_hip_kernel_timing(1)
+    # graph replays record no per-kernel events: the dominant kernel is then
+    # timed in an eager pass of the same length after the timed region
+    hip().ds3_hip_kernel_timing(0 if graph else 1)
     hip().ds3_hip_synchronize()
     hip().ds3_hip_begin_batch()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        token(i)
+        step(i)
     hip().ds3_hip_end_batch()
     wall_ms = (time.perf_counter() - t0) * 1e3
+    if graph:
+        hip().ds3_hip_kernel_timing(1)
+        hip().ds3_hip_begin_batch()
+        for i in range(args.steps):
+            token(i)
+        hip().ds3_hip_end_batch()
+        graph.close()
     hip().ds3_hip_kernel_timing(0)
     hip().ds3_hip_kernel_timing_only(None)
     stats = ds3.kernel_stats()
     ms = wall_ms / args.steps
-    log(f"[bench] config 4: {ms * 1e3:.1f} us/token through {L} layers ({ms * 1e3 / L:.2f} us/layer)")
+    log(f"[bench] config 4: {ms * 1e3:.1f} us/token through {L} layers ({ms * 1e3 / L:.2f} us/layer)"
+        + (", layers replayed as one HIP graph" if graph else ""))
     log_breakdown(brk, stats)
     b = L * W.algorithmic_bytes(spec, 1, n_used)
     tpath = Path(args.traffic) if args.traffic else ROOT / "profiles" / "hbm_traffic.json"
@@ -289,7 +324,8 @@ def run_stack(args, n_used=8):
         "config": {"workload": f"configs[3]: decode, one token through {L} resident Qwen3-30B-A3B MoE-FFN layers, "
                                + ("h <- h + MoE_l(rms_norm(h) * g_l) (the engine's FFN block); " if args.stack_block
                                   else "h <- h + MoE_l(h); ")
-                               + "Q4_K gate/up + Q6_K down, F32 router",
+                               + "Q4_K gate/up + Q6_K down, F32 router"
+                               + ("" if args.no_graph else "; layers replayed as one HIP graph"),
                    "tokens": 1, "layers": L, "n_embd": K, "n_ff": spec.n_ff},
         "roofline": roofline(stats, spec, 1, counts, n_used, traffic),
         "alg_bytes_per_step": b,

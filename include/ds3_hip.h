@@ -298,6 +298,21 @@ double ds3_hip_timer_stop_ms(void);
 /* Device name (e.g. "gfx950"), compute-unit count and HBM bytes. */
 int ds3_hip_device_info(char *arch, size_t arch_len, int *n_cu, uint64_t *hbm_bytes);
 
+/* HIP graphs (no ds3_metal.h counterpart; for callers that replay the same
+ * calls many times, such as a decode step through every layer).  The calls
+ * made between graph_begin and graph_end are captured on the library's
+ * stream instead of run: they wait for nothing, nothing may be read back,
+ * and the library's workspace must already be large enough (make the same
+ * calls once before capturing; a call that would grow it fails).  The
+ * captured calls hold no memset nodes.  graph_end returns an executable
+ * graph; each graph_launch replays it on the library's stream with the
+ * buffers the calls named (synchronous outside begin_batch / end_batch).
+ * Not allowed while in batch mode or with kernel timing on. */
+int  ds3_hip_graph_begin(void);
+int  ds3_hip_graph_end(void **graph);
+int  ds3_hip_graph_launch(void *graph);
+void ds3_hip_graph_destroy(void *graph);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,6 +50,7 @@ struct State {
     bool inited = false;
     hipStream_t stream = nullptr;
     bool batch = false;
+    bool capturing = false;          // between ds3_hip_graph_begin and ds3_hip_graph_end
     uint8_t *ws = nullptr;
     size_t ws_bytes = 0;
     int32_t *zero_idx = nullptr;     // device {0}
@@ -109,6 +110,11 @@ int finish(hipError_t e, const char *what)
 uint8_t *ws_get(size_t bytes)
 {
     if (bytes <= g.ws_bytes) return g.ws;
+    if (g.capturing) {
+        fprintf(stderr, "ds3_hip: a captured call needs %zu workspace bytes (have %zu): make the same call once "
+                        "before ds3_hip_graph_begin\n", bytes, g.ws_bytes);
+        return nullptr;
+    }
     if (g.ws) {
         (void)hipStreamSynchronize(g.stream);
         (void)hipFree(g.ws);
@@ -1274,6 +1280,55 @@ extern "C" void ds3_hip_end_batch(void)
     g.batch = false;
 }
 
+// ===========================================================================
+// HIP graphs (no ds3_metal.h counterpart): stream capture of library calls
+// ===========================================================================
+
+extern "C" int ds3_hip_graph_begin(void)
+{
+    if (!ensure_init()) return -1;
+    if (g.batch || g.capturing) {
+        fprintf(stderr, "ds3_hip: graph_begin inside batch mode or another capture\n");
+        return -1;
+    }
+    if (g.ktiming) {
+        fprintf(stderr, "ds3_hip: graph_begin with kernel timing on\n");
+        return -1;
+    }
+    if (report(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal), "graph_begin") != 0) return -1;
+    g.capturing = true;
+    g.batch = true;                  // calls enqueue without waiting
+    return 0;
+}
+
+extern "C" int ds3_hip_graph_end(void **graph)
+{
+    if (!g.capturing) return -1;
+    hipGraph_t gr = nullptr;
+    const hipError_t e = hipStreamEndCapture(g.stream, &gr);
+    g.capturing = false;
+    g.batch = false;
+    if (report(e, "graph_end") != 0 || gr == nullptr) return -1;
+    hipGraphExec_t ex = nullptr;
+    const hipError_t ei = hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(gr);
+    if (report(ei, "graph_end (instantiate)") != 0) return -1;
+    if (graph) *graph = (void *)ex;
+    else (void)hipGraphExecDestroy(ex);
+    return 0;
+}
+
+extern "C" int ds3_hip_graph_launch(void *graph)
+{
+    if (!graph || g.capturing || !ensure_init()) return -1;
+    return finish(hipGraphLaunch((hipGraphExec_t)graph, g.stream), "graph_launch");
+}
+
+extern "C" void ds3_hip_graph_destroy(void *graph)
+{
+    if (graph) (void)hipGraphExecDestroy((hipGraphExec_t)graph);
+}
+
 extern "C" void ds3_hip_synchronize(void)
 {
     if (g.inited) (void)hipStreamSynchronize(g.stream);
@@ -1296,6 +1351,10 @@ extern "C" void ds3_hip_profile_print(const char *label)
 extern "C" void ds3_hip_kernel_timing(int enable)
 {
     if (!ensure_init()) return;
+    if (enable && g.capturing) {
+        fprintf(stderr, "ds3_hip: kernel timing cannot start during graph capture\n");
+        return;
+    }
     if (enable && g.pool.empty()) {
         g.pool.resize(16384);
         for (auto &e : g.pool) (void)hipEventCreate(&e);

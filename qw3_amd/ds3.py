@@ -194,6 +194,41 @@ def moe_ffn(x: Buffer, router: Buffer, router_type: int, ex: ExpertTensors, out:
         "moe_ffn")
 
 
+class Graph:
+    """Calls made inside `with ds3.Graph() as gr:` are captured, not run;
+    gr.launch() replays them (ds3_hip_graph_begin / _end / _launch)."""
+
+    def __init__(self):
+        self.handle = None
+
+    def __enter__(self) -> "Graph":
+        _check(hip().ds3_hip_graph_begin(), "graph_begin")
+        return self
+
+    def __exit__(self, exc_type, exc, tb) -> None:
+        h = C.c_void_p()
+        rc = hip().ds3_hip_graph_end(C.byref(h))
+        if exc_type is None:
+            _check(rc, "graph_end")
+            self.handle = h.value
+        elif rc == 0 and h.value:
+            hip().ds3_hip_graph_destroy(h.value)
+
+    def launch(self) -> None:
+        _check(hip().ds3_hip_graph_launch(self.handle), "graph_launch")
+
+    def close(self) -> None:
+        if self.handle:
+            hip().ds3_hip_graph_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def set_prefill_min_tokens(n: int) -> int:
     return hip().ds3_hip_set_prefill_min_tokens(n)
 

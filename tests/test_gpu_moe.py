@@ -781,3 +781,41 @@ def test_moe_ffn_batch_in_place(hip_ready, real, T):
     got = hb.read(np.float32, (T, s.n_embd))
     # h + (w_1 y_1 + ...) rounds after each of the 8 adds at |h|'s scale instead of once
     np.testing.assert_allclose(got, want, rtol=0, atol=8 * float(np.spacing(np.abs(want).max())))
+
+
+@pytest.mark.parametrize("T", [1, 64])
+def test_graph_replay(hip_ready, real, T):
+    """A captured zero + moe_ffn_batch (decode path with the fused selection at
+    T = 1, grouped path at T = 64) replayed three times, with eager calls on
+    other buffers and synchronisations between the replays: every replay
+    rewrites the poisoned output with exactly the eager result."""
+    from qw3_amd._native import hip
+    s = real.spec
+    xb = ds3.Buffer.from_array(W.make_inputs(2, T, seed=130))
+    out, idx = ds3.Buffer.alloc(T * s.n_embd * 4), ds3.Buffer.alloc(T * W.N_USED * 4)
+    xo, oo = ds3.Buffer.from_array(W.make_inputs(2, T, seed=131)), ds3.Buffer.alloc(T * s.n_embd * 4)
+
+    def call(x, o, ix=None):
+        o.zero()                                   # a fill kernel, not a memset node
+        ds3.moe_ffn_batch(x, real.dev.router, s.router_type, real.dev.experts, o, T, s.n_expert, W.N_USED,
+                          indices=ix)
+
+    print(f"  graph replay T={T}", flush=True)
+    call(xb, out, idx)
+    want, want_i = out.read(np.float32, (T, s.n_embd)), idx.read(np.int32, (T, W.N_USED))
+    call(xo, oo)
+    want_o = oo.read(np.float32, (T, s.n_embd))
+    with ds3.Graph() as gr:
+        call(xb, out, idx)
+    try:
+        for rep in range(3):
+            out.write(np.full((T, s.n_embd), 7.0, np.float32))
+            idx.write(np.full((T, W.N_USED), -1, np.int32))
+            gr.launch()
+            assert np.array_equal(out.read(np.float32, (T, s.n_embd)), want), f"replay {rep}"
+            assert np.array_equal(idx.read(np.int32, (T, W.N_USED)), want_i), f"replay {rep}"
+            call(xo, oo)                           # eager work between the replays
+            hip().ds3_hip_synchronize()
+            assert np.array_equal(oo.read(np.float32, (T, s.n_embd)), want_o)
+    finally:
+        gr.close()
