@@ -307,7 +307,19 @@ int ds3_hip_device_info(char *arch, size_t arch_len, int *n_cu, uint64_t *hbm_by
  * captured calls hold no memset nodes.  graph_end returns an executable
  * graph; each graph_launch replays it on the library's stream with the
  * buffers the calls named (synchronous outside begin_batch / end_batch).
- * Not allowed while in batch mode or with kernel timing on. */
+ * Not allowed while in batch mode or with kernel timing on.  During a capture
+ * every entry point that would allocate, free, copy from or to the host or
+ * wait (buffer_alloc / from_mmap / write / read, moe_ffn_experts,
+ * synchronize, end_batch, router_stats, the timers, graph_launch) returns -1
+ * (or does nothing) with a diagnostic; buffer_free is deferred to graph_end.
+ * A live graph (graph_end .. graph_destroy) keeps the workspace block its
+ * kernels address: a later eager call that needs a larger workspace gets a
+ * new block and the old one is freed when the last live graph is destroyed.
+ * Buffers the captured calls named must outlive the graph.  ds3_hip_shutdown
+ * destroys every live graph. */
+/* Test hook for the capture refusals above: marks a capture as open (on = 1)
+ * or closed (0) without a device.  Refused (-1) once ds3_hip_init has run. */
+int  ds3_hip_debug_simulate_capture(int on);
 int  ds3_hip_graph_begin(void);
 int  ds3_hip_graph_end(void **graph);
 int  ds3_hip_graph_launch(void *graph);

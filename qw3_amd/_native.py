@@ -54,6 +54,7 @@ SIGNATURES: dict[str, tuple] = {
     "ds3_hip_moe_router_topk_batch_tokens": (C.c_int, [P, P, P, U32, U32, U32, U32, B]),
     "ds3_hip_begin_batch": (C.c_int, []),
     "ds3_hip_end_batch": (None, []),
+    "ds3_hip_debug_simulate_capture": (C.c_int, [C.c_int]),
     "ds3_hip_graph_begin": (C.c_int, []),
     "ds3_hip_graph_end": (C.c_int, [C.POINTER(C.c_void_p)]),
     "ds3_hip_graph_launch": (C.c_int, [P]),

@@ -53,6 +53,9 @@ struct State {
     bool capturing = false;          // between ds3_hip_graph_begin and ds3_hip_graph_end
     uint8_t *ws = nullptr;
     size_t ws_bytes = 0;
+    std::vector<void *> graphs;      // live executable graphs (graph_end .. graph_destroy)
+    std::vector<uint8_t *> retired;  // workspace blocks outgrown while a live graph may address them
+    std::vector<ds3_hip_buffer_t *> deferred_free;   // buffers freed during a capture
     int32_t *zero_idx = nullptr;     // device {0}
     int32_t *tickets = nullptr;      // kTickets router tickets (zero between launches)
     int router_mode = 0;             // ds3_hip_set_router_mode
@@ -105,8 +108,21 @@ int finish(hipError_t e, const char *what)
     return 0;
 }
 
+// Refuse an entry point that would synchronise, copy from the host or
+// allocate while a graph capture is open on the library stream: any of those
+// would break the capture or record a node that replays stale host data.
+bool refuse_in_capture(const char *what)
+{
+    if (!g.capturing) return false;
+    fprintf(stderr, "ds3_hip: %s is not allowed during graph capture (ds3_hip_graph_begin .. ds3_hip_graph_end)\n",
+            what);
+    return true;
+}
+
 // Device workspace, grown on demand.  Growing waits for queued work that may
-// still use the old block.
+// still use the old block.  While an executable graph is alive the old block
+// is retired instead of freed (the graph's kernels address it); retired blocks
+// are freed once the last live graph is destroyed.
 uint8_t *ws_get(size_t bytes)
 {
     if (bytes <= g.ws_bytes) return g.ws;
@@ -117,7 +133,8 @@ uint8_t *ws_get(size_t bytes)
     }
     if (g.ws) {
         (void)hipStreamSynchronize(g.stream);
-        (void)hipFree(g.ws);
+        if (g.graphs.empty()) (void)hipFree(g.ws);
+        else g.retired.push_back(g.ws);
         g.ws = nullptr;
         g.ws_bytes = 0;
     }
@@ -130,6 +147,26 @@ uint8_t *ws_get(size_t bytes)
     g.ws_bytes = want;
     return g.ws;
 }
+
+// Buffers whose ds3_hip_buffer_free came during the capture that just ended.
+void free_deferred()
+{
+    std::vector<ds3_hip_buffer_t *> v;
+    v.swap(g.deferred_free);
+    for (ds3_hip_buffer_t *b : v) ds3_hip_buffer_free(b);
+}
+
+// Workspace blocks retired while graphs were alive, once none is left.
+void free_retired()
+{
+    if (!g.graphs.empty() || g.retired.empty()) return;
+    (void)hipStreamSynchronize(g.stream);
+    for (uint8_t *p : g.retired) (void)hipFree(p);
+    g.retired.clear();
+}
+
+bool graph_live(void *graph) { return std::find(g.graphs.begin(), g.graphs.end(), graph) != g.graphs.end(); }
+
 
 struct Bump {
     size_t off = 0;
@@ -164,6 +201,19 @@ struct KScope {
 };
 
 bool is_quant(int t) { return t == T_Q4_K || t == T_Q6_K || t == T_Q8_0; }
+
+// Bytes of one row of n values of a weight type (0 for an unknown type).
+size_t row_bytes(int type, uint32_t n)
+{
+    switch (type) {
+    case T_F32: return (size_t)n * 4;
+    case T_F16: return (size_t)n * 2;
+    case T_Q8_0: return (size_t)n / 32 * 34;
+    case T_Q4_K: return (size_t)n / 256 * 144;
+    case T_Q6_K: return (size_t)n / 256 * 210;
+    default: return 0;
+    }
+}
 
 // reference src/ds3_metal.m:1841-1862
 bool quant_type_ok_for_moe(int type, uint32_t in_dim, const char *name)
@@ -291,7 +341,19 @@ extern "C" int ds3_hip_init(void)
 extern "C" void ds3_hip_shutdown(void)
 {
     if (!g.inited) return;
+    if (g.capturing) {                       // abandon an open capture
+        hipGraph_t gr = nullptr;
+        if (hipStreamEndCapture(g.stream, &gr) == hipSuccess && gr) (void)hipGraphDestroy(gr);
+        g.capturing = false;
+        g.batch = false;
+        free_deferred();
+    }
     (void)hipStreamSynchronize(g.stream);
+    // graphs address the workspace freed below: they end with the context
+    for (void *gr : g.graphs) (void)hipGraphExecDestroy((hipGraphExec_t)gr);
+    g.graphs.clear();
+    for (uint8_t *p : g.retired) (void)hipFree(p);
+    g.retired.clear();
     for (hipEvent_t e : g.pool) (void)hipEventDestroy(e);
     g.pool.clear();
     g.recs.clear();
@@ -311,7 +373,7 @@ extern "C" void ds3_hip_shutdown(void)
 
 extern "C" ds3_hip_buffer_t *ds3_hip_buffer_alloc(size_t bytes)
 {
-    if (bytes == 0 || !ensure_init()) return nullptr;
+    if (bytes == 0 || refuse_in_capture("buffer_alloc") || !ensure_init()) return nullptr;
     void *p = nullptr;
     const size_t padded = ((bytes + 255) & ~(size_t)255) + kAllocPad;
     if (hipMalloc(&p, padded) != hipSuccess) return nullptr;
@@ -333,7 +395,7 @@ extern "C" ds3_hip_buffer_t *ds3_hip_buffer_alloc(size_t bytes)
 
 extern "C" ds3_hip_buffer_t *ds3_hip_buffer_from_mmap(const void *base, size_t bytes)
 {
-    if (!base || bytes == 0) return nullptr;
+    if (!base || bytes == 0 || refuse_in_capture("buffer_from_mmap")) return nullptr;
     long ps = sysconf(_SC_PAGESIZE);
     if (ps <= 0) ps = 4096;
     if (((uintptr_t)base) & ((uintptr_t)ps - 1)) {
@@ -362,6 +424,11 @@ extern "C" ds3_hip_buffer_t *ds3_hip_buffer_view(const ds3_hip_buffer_t *base, s
 extern "C" void ds3_hip_buffer_free(ds3_hip_buffer_t *buf)
 {
     if (!buf) return;
+    if (g.capturing) {
+        // freeing waits for the stream, which a capture forbids: free it when the capture ends
+        g.deferred_free.push_back(buf);
+        return;
+    }
     if (buf->owner && buf->base) {
         if (g.inited) (void)hipStreamSynchronize(g.stream);
         (void)hipFree(buf->base);
@@ -371,7 +438,11 @@ extern "C" void ds3_hip_buffer_free(ds3_hip_buffer_t *buf)
 
 extern "C" int ds3_hip_buffer_write(ds3_hip_buffer_t *buf, size_t offset, const void *src, size_t bytes)
 {
-    if (!buf || !src || offset + bytes > buf->bytes || buf->readonly) return -1;
+    if (!buf || !src || offset + bytes > buf->bytes || refuse_in_capture("buffer_write")) return -1;
+    if (buf->readonly) {
+        fprintf(stderr, "ds3_hip: buffer_write into a buffer imported with buffer_from_mmap is refused\n");
+        return -1;
+    }
     if (bytes == 0) return 0;
     hipError_t e = hipMemcpyAsync(buf->base + buf->offset + offset, src, bytes, hipMemcpyHostToDevice, g.stream);
     if (e == hipSuccess) e = hipStreamSynchronize(g.stream);
@@ -380,7 +451,7 @@ extern "C" int ds3_hip_buffer_write(ds3_hip_buffer_t *buf, size_t offset, const 
 
 extern "C" int ds3_hip_buffer_read(ds3_hip_buffer_t *buf, size_t offset, void *dst, size_t bytes)
 {
-    if (!buf || !dst || offset + bytes > buf->bytes) return -1;
+    if (!buf || !dst || offset + bytes > buf->bytes || refuse_in_capture("buffer_read")) return -1;
     if (bytes == 0) return 0;
     hipError_t e = hipMemcpyAsync(dst, buf->base + buf->offset + offset, bytes, hipMemcpyDeviceToHost, g.stream);
     if (e == hipSuccess) e = hipStreamSynchronize(g.stream);
@@ -864,7 +935,21 @@ extern "C" int ds3_hip_moe_ffn_experts(
                        !quant_type_ok_for_moe(shared_up_type, n_embd, "shared_up") ||
                        !quant_type_ok_for_moe(shared_down_type, n_ff_shared, "shared_down")))
         return -1;
-    if (n_used > 16 || !ensure_init()) return -1;
+    if (n_used > 16 || refuse_in_capture("moe_ffn_experts (copies the host's indices and scores)") || !ensure_init())
+        return -1;
+    if (!fits(input, (size_t)n_embd * 4, "input") || !fits(output, (size_t)n_embd * 4, "output")) return -1;
+    if (has_shared) {
+        const int sgt = shared_gate_type, sut = shared_up_type, sdt = shared_down_type;
+        if (!fits(w_shared_gate, (size_t)n_ff_shared * shared_gate_row_stride, "shared_gate") ||
+            !fits(w_shared_up, (size_t)n_ff_shared * shared_up_row_stride, "shared_up") ||
+            !fits(w_shared_down, (size_t)n_embd * shared_down_row_stride, "shared_down") ||
+            shared_gate_row_stride < (uint64_t)row_bytes(sgt, n_embd) ||
+            shared_up_row_stride < (uint64_t)row_bytes(sut, n_embd) ||
+            shared_down_row_stride < (uint64_t)row_bytes(sdt, n_ff_shared)) {
+            fprintf(stderr, "ds3_hip: moe_ffn_experts: shared expert weights smaller than their shapes\n");
+            return -1;
+        }
+    }
     // Host-selected expert ids must address rows inside every expert tensor.
     {
         const uint64_t ne_g = gate_row_stride ? w_gate_exps->bytes / ((uint64_t)n_ff_exp * gate_row_stride) : 0;
@@ -1220,7 +1305,7 @@ extern "C" int ds3_hip_dequantize(const ds3_hip_buffer_t *src, uint64_t src_offs
 
 extern "C" int ds3_hip_router_stats(uint64_t *certified, uint64_t *repaired, int reset)
 {
-    if (!ensure_init()) return -1;
+    if (refuse_in_capture("router_stats") || !ensure_init()) return -1;
     unsigned long long v[2] = { 0, 0 };
     if (hipStreamSynchronize(g.stream) != hipSuccess ||
         hipMemcpy(v, g.cert_stats, sizeof v, hipMemcpyDeviceToHost) != hipSuccess)
@@ -1265,7 +1350,7 @@ extern "C" int ds3_hip_begin_batch(void)
 
 extern "C" void ds3_hip_end_batch(void)
 {
-    if (!g.batch) return;
+    if (!g.batch || refuse_in_capture("end_batch")) return;
     if (g.profile) (void)hipEventRecord(g.bev1, g.stream);
     const auto c0 = std::chrono::steady_clock::now();
     (void)hipStreamSynchronize(g.stream);
@@ -1301,6 +1386,7 @@ extern "C" int ds3_hip_graph_begin(void)
     return 0;
 }
 
+
 extern "C" int ds3_hip_graph_end(void **graph)
 {
     if (!g.capturing) return -1;
@@ -1308,30 +1394,51 @@ extern "C" int ds3_hip_graph_end(void **graph)
     const hipError_t e = hipStreamEndCapture(g.stream, &gr);
     g.capturing = false;
     g.batch = false;
+    free_deferred();
     if (report(e, "graph_end") != 0 || gr == nullptr) return -1;
     hipGraphExec_t ex = nullptr;
     const hipError_t ei = hipGraphInstantiate(&ex, gr, nullptr, nullptr, 0);
     (void)hipGraphDestroy(gr);
     if (report(ei, "graph_end (instantiate)") != 0) return -1;
-    if (graph) *graph = (void *)ex;
-    else (void)hipGraphExecDestroy(ex);
+    if (graph) {
+        *graph = (void *)ex;
+        g.graphs.push_back((void *)ex);          // pins the workspace block its kernels address
+    } else {
+        (void)hipGraphExecDestroy(ex);
+    }
+    return 0;
+}
+
+extern "C" int ds3_hip_debug_simulate_capture(int on)
+{
+    // only without a device context, where no real capture can be open
+    if (g.inited) return -1;
+    g.capturing = on != 0;
     return 0;
 }
 
 extern "C" int ds3_hip_graph_launch(void *graph)
 {
-    if (!graph || g.capturing || !ensure_init()) return -1;
+    if (!graph || refuse_in_capture("graph_launch") || !ensure_init()) return -1;
+    if (!graph_live(graph)) {
+        fprintf(stderr, "ds3_hip: graph_launch of a graph that graph_end did not return or that was destroyed\n");
+        return -1;
+    }
     return finish(hipGraphLaunch((hipGraphExec_t)graph, g.stream), "graph_launch");
 }
 
 extern "C" void ds3_hip_graph_destroy(void *graph)
 {
-    if (graph) (void)hipGraphExecDestroy((hipGraphExec_t)graph);
+    if (!graph || !graph_live(graph)) return;
+    if (g.inited) (void)hipStreamSynchronize(g.stream);     // a replay may still be running
+    (void)hipGraphExecDestroy((hipGraphExec_t)graph);
+    g.graphs.erase(std::find(g.graphs.begin(), g.graphs.end(), graph));
+    free_retired();
 }
 
 extern "C" void ds3_hip_synchronize(void)
 {
-    if (g.inited) (void)hipStreamSynchronize(g.stream);
+    if (g.inited && !refuse_in_capture("synchronize")) (void)hipStreamSynchronize(g.stream);
 }
 
 extern "C" void ds3_hip_profile_reset(void)
@@ -1369,6 +1476,7 @@ extern "C" void ds3_hip_kernel_timing_only(const char *name)
 
 extern "C" void ds3_hip_kernel_timing_reset(void)
 {
+    if (refuse_in_capture("kernel_timing_reset")) return;
     if (g.inited) (void)hipStreamSynchronize(g.stream);
     g.recs.clear();
     g.pool_used = 0;
@@ -1380,7 +1488,7 @@ extern "C" void ds3_hip_kernel_timing_reset(void)
 
 extern "C" int ds3_hip_kernel_stats(int i, char *name, size_t name_len, int64_t *count, double *total_ms)
 {
-    if (!g.inited) return -1;
+    if (!g.inited || refuse_in_capture("kernel_stats")) return -1;
     if (g.stats_dirty) {
         (void)hipStreamSynchronize(g.stream);
         g.stat_names.clear();
@@ -1413,13 +1521,13 @@ extern "C" int ds3_hip_kernel_stats(int i, char *name, size_t name_len, int64_t 
 
 extern "C" int ds3_hip_timer_start(void)
 {
-    if (!ensure_init()) return -1;
+    if (refuse_in_capture("timer_start") || !ensure_init()) return -1;
     return report(hipEventRecord(g.t0, g.stream), "timer_start");
 }
 
 extern "C" double ds3_hip_timer_stop_ms(void)
 {
-    if (!g.inited) return -1.0;
+    if (!g.inited || refuse_in_capture("timer_stop_ms")) return -1.0;
     (void)hipEventRecord(g.t1, g.stream);
     (void)hipEventSynchronize(g.t1);
     float ms = 0.f;
@@ -1429,7 +1537,7 @@ extern "C" double ds3_hip_timer_stop_ms(void)
 
 extern "C" int ds3_hip_device_info(char *arch, size_t arch_len, int *n_cu, uint64_t *hbm_bytes)
 {
-    if (!ensure_init()) return -1;
+    if (refuse_in_capture("device_info") || !ensure_init()) return -1;
     hipDeviceProp_t p;
     if (hipGetDeviceProperties(&p, 0) != hipSuccess) return -1;
     if (arch && arch_len) {
