@@ -241,6 +241,31 @@ int ds3_hip_moe_block(
     uint32_t n_tokens, uint32_t n_embd, uint32_t n_expert, uint32_t n_used, uint32_t n_ff_exp,
     uint64_t router_row_stride, ds3_hip_type_t router_type, bool norm_topk_prob);
 
+/* ds3_hip_moe_ffn_batch that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, semantics and results as ds3_hip_moe_ffn_batch; every
+ * intermediate (routing rows, bucketing lists, h, y) lives in one library-owned
+ * scratch array of ds3_hip_noalloc_scratch_bytes() bytes per GPU (64 MiB: a
+ * Qwen3-30B-A3B layer call of up to 785 tokens), held until the process ends.
+ * A call whose intermediates do not fit returns -1 with a diagnostic; split it
+ * into fewer tokens.  ds3_hip_init must have been called.  Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (from several host
+ * threads, or a graph replay with an eager call of this entry point on another
+ * stream) race.  The array keeps the last call's contents; no kernel reads a
+ * byte of it before the same call has written it. */
+int ds3_hip_moe_ffn_batch_noalloc(
+    const ds3_hip_buffer_t *input, const ds3_hip_buffer_t *w_gate_inp,
+    const ds3_hip_buffer_t *w_gate_exps, const ds3_hip_buffer_t *w_up_exps, const ds3_hip_buffer_t *w_down_exps,
+    ds3_hip_type_t gate_type, ds3_hip_type_t up_type, ds3_hip_type_t down_type,
+    uint64_t gate_row_stride, uint64_t up_row_stride, uint64_t down_row_stride,
+    const ds3_hip_buffer_t *expert_offsets,
+    ds3_hip_buffer_t *output, const ds3_hip_buffer_t *residual,
+    ds3_hip_buffer_t *gate_logits, ds3_hip_buffer_t *indices, ds3_hip_buffer_t *scores,
+    uint32_t n_tokens, uint32_t n_embd, uint32_t n_expert, uint32_t n_used, uint32_t n_ff_exp,
+    uint64_t router_row_stride, ds3_hip_type_t router_type, bool norm_topk_prob);
+size_t ds3_hip_noalloc_scratch_bytes(void);
+
 /* Router only, for T tokens: logits (bit-identical to the reference's
  * sequential fp32 sums), then indices/scores [T][n_used]. */
 int ds3_hip_moe_route(const ds3_hip_buffer_t *input, const ds3_hip_buffer_t *w_gate_inp,

@@ -64,6 +64,9 @@ SIGNATURES: dict[str, tuple] = {
     "ds3_hip_profile_print": (None, [CP]),
     "ds3_hip_moe_ffn_batch": (C.c_int, [P, P, P, P, P, I32, I32, I32, U64, U64, U64, P,
                                         P, P, P, P, P, U32, U32, U32, U32, U32, U64, I32, B]),
+    "ds3_hip_moe_ffn_batch_noalloc": (C.c_int, [P, P, P, P, P, I32, I32, I32, U64, U64, U64, P,
+                                                P, P, P, P, P, U32, U32, U32, U32, U32, U64, I32, B]),
+    "ds3_hip_noalloc_scratch_bytes": (SZ, []),
     "ds3_hip_moe_block": (C.c_int, [P, P, F, P, P, P, P, I32, I32, I32, U64, U64, U64, P,
                                     P, P, P, P, U32, U32, U32, U32, U32, U64, I32, B]),
     "ds3_hip_moe_route": (C.c_int, [P, P, P, P, P, U32, U32, U32, U32, U64, I32, B]),

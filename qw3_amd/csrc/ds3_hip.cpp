@@ -27,6 +27,16 @@ struct ds3_hip_buffer {
 
 using namespace ds3k;
 
+// Scratch of the allocation-free entry point ds3_hip_moe_ffn_batch_noalloc:
+// every buffer a call of that entry point needs beyond its inputs and outputs
+// (routing rows, bucketing lists, h, y) is carved from this array.  Each GPU
+// the library runs on holds its own copy until the process ends.  Host code
+// never passes `scratch` itself to a kernel (on the host the name is only a
+// stand-in): ds3_hip_init looks up its device address once per device and the
+// entry point passes that.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
 namespace {
 
 constexpr int kDefaultPrefillMin = 16;
@@ -40,6 +50,7 @@ constexpr int kFuseSelMaxTokens = DS3_FUSE_SELECT_MAX_T;
 #define DS3_FUSED_NB 4                   // repair batch rows of the fused selection at T <= 2
 #endif
 constexpr size_t kAllocPad = 256;        // slack after every allocation: kernels read whole dwords
+constexpr int kMaxDevices = 64;
 
 struct KRec {
     const char *name;
@@ -56,6 +67,8 @@ struct State {
     std::vector<void *> graphs;      // live executable graphs (graph_end .. graph_destroy)
     std::vector<uint8_t *> retired;  // workspace blocks outgrown while a live graph may address them
     std::vector<ds3_hip_buffer_t *> deferred_free;   // buffers freed during a capture
+    int device = 0;                  // the device the context runs on
+    uint8_t *scratch_dev[kMaxDevices] = {};   // device address of `scratch` per device, from ds3_hip_init
     int32_t *zero_idx = nullptr;     // device {0}
     int32_t *tickets = nullptr;      // kTickets router tickets (zero between launches)
     int router_mode = 0;             // ds3_hip_set_router_mode
@@ -311,9 +324,20 @@ extern "C" int ds3_hip_init(void)
         return -1;
     }
     if (hipSetDevice(0) != hipSuccess) return -1;
+    g.device = 0;
     if (hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking) != hipSuccess) {
         fprintf(stderr, "ds3_hip: stream creation failed\n");
         return -1;
+    }
+    if (g.scratch_dev[g.device] == nullptr) {
+        // with the device current: this device's copy of the scratch array
+        void *sp = nullptr;
+        const hipError_t es = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+        if (es != hipSuccess || sp == nullptr) {
+            fprintf(stderr, "ds3_hip: scratch array lookup failed: %s\n", hipGetErrorString(es));
+            return -1;
+        }
+        g.scratch_dev[g.device] = (uint8_t *)sp;
     }
     void *consts = nullptr;
     if (hipMalloc(&consts, 128 + (size_t)kTickets * 4 + 16) != hipSuccess) return -1;
@@ -364,7 +388,10 @@ extern "C" void ds3_hip_shutdown(void)
     if (g.ws) (void)hipFree(g.ws);
     (void)hipFree(g.zero_idx);
     (void)hipStreamDestroy(g.stream);
+    uint8_t *sd[kMaxDevices];
+    std::copy(g.scratch_dev, g.scratch_dev + kMaxDevices, sd);
     g = State();
+    std::copy(sd, sd + kMaxDevices, g.scratch_dev);      // the arrays outlive the context
 }
 
 // ===========================================================================
@@ -1094,9 +1121,17 @@ struct NormIn {
     float *xn;
 };
 
+// A caller-fixed workspace (the allocation-free entry point's scratch array):
+// moe_batch uses it instead of growing the library workspace.
+struct WsFixed {
+    uint8_t *base;
+    size_t cap;
+};
+
 // The batch MoE of ds3_hip_moe_ffn_batch / ds3_hip_moe_block on raw device
 // rows: input x_in [T][n_embd]; out (+)= result (+ residual res); the routing
-// outputs (logits, indices, scores) are optional.
+// outputs (logits, indices, scores) are optional.  With `fixed`, the call's
+// workspace is fixed->base and a call that needs more fails.
 int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_gate_inp,
               const ds3_hip_buffer_t *w_gate_exps, const ds3_hip_buffer_t *w_up_exps,
               const ds3_hip_buffer_t *w_down_exps, ds3_hip_type_t gate_type, ds3_hip_type_t up_type,
@@ -1104,7 +1139,7 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
               const ds3_hip_buffer_t *expert_offsets, float *out, const float *res, float *logits_out,
               int32_t *idx_out, float *scores_out, uint32_t n_tokens, uint32_t n_embd, uint32_t n_expert,
               uint32_t n_used, uint32_t n_ff_exp, uint64_t router_row_stride, ds3_hip_type_t router_type,
-              bool norm_topk_prob, const char *what)
+              bool norm_topk_prob, const char *what, const WsFixed *fixed = nullptr)
 {
     if (!w_gate_inp || !w_gate_exps || !w_up_exps || !w_down_exps) return -1;
     if (n_tokens == 0 || n_embd == 0 || n_expert == 0 || n_used == 0 || n_ff_exp == 0 || n_used > n_expert)
@@ -1149,7 +1184,18 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
         o_h = bp.take(T * n_used * n_ff_exp * 4);
         o_t = bp.take(T * n_used * n_ff_exp * 4);
     }
-    uint8_t *ws = ws_get(bp.off);
+    uint8_t *ws = nullptr;
+    if (fixed) {
+        if (bp.off > fixed->cap) {
+            fprintf(stderr, "ds3_hip: %s: %u tokens need %zu scratch bytes, more than the %zu the allocation-free "
+                            "entry point holds (split the call into fewer tokens)\n",
+                    what, n_tokens, bp.off, fixed->cap);
+            return -1;
+        }
+        ws = fixed->base;
+    } else {
+        ws = ws_get(bp.off);
+    }
     if (!ws) return -1;
     const RouteBufs rb = route_bufs(ws + o_w, rs, logits_out ? logits_out : (float *)(ws + o_l),
                                     idx_out ? idx_out : (int32_t *)(ws + o_i), scores_out ? scores_out : (float *)(ws + o_s),
@@ -1246,6 +1292,39 @@ extern "C" int ds3_hip_moe_ffn_batch(
                      indices ? (int32_t *)dptr(indices) : nullptr, scores ? fptr(scores) : nullptr, n_tokens, n_embd,
                      n_expert, n_used, n_ff_exp, router_row_stride, router_type, norm_topk_prob, "moe_ffn_batch");
 }
+
+// ds3_hip_moe_ffn_batch with every intermediate in the library's `scratch`
+// array: no allocation of any kind.  No reference counterpart.
+extern "C" int ds3_hip_moe_ffn_batch_noalloc(
+    const ds3_hip_buffer_t *input, const ds3_hip_buffer_t *w_gate_inp, const ds3_hip_buffer_t *w_gate_exps,
+    const ds3_hip_buffer_t *w_up_exps, const ds3_hip_buffer_t *w_down_exps, ds3_hip_type_t gate_type,
+    ds3_hip_type_t up_type, ds3_hip_type_t down_type, uint64_t gate_row_stride, uint64_t up_row_stride,
+    uint64_t down_row_stride, const ds3_hip_buffer_t *expert_offsets, ds3_hip_buffer_t *output,
+    const ds3_hip_buffer_t *residual, ds3_hip_buffer_t *gate_logits, ds3_hip_buffer_t *indices,
+    ds3_hip_buffer_t *scores, uint32_t n_tokens, uint32_t n_embd, uint32_t n_expert, uint32_t n_used,
+    uint32_t n_ff_exp, uint64_t router_row_stride, ds3_hip_type_t router_type, bool norm_topk_prob)
+{
+    if (!input || !output) return -1;
+    if (!g.inited) {
+        // initialising allocates (stream, constants): callers that cannot allocate initialise first
+        fprintf(stderr, "ds3_hip: moe_ffn_batch_noalloc needs ds3_hip_init first\n");
+        return -1;
+    }
+    const size_t T = n_tokens;
+    if (!fits(input, T * n_embd * 4, "input") || !fits(output, T * n_embd * 4, "output") ||
+        !fits(residual, T * n_embd * 4, "residual") || !fits(gate_logits, T * n_expert * 4, "gate_logits") ||
+        !fits(indices, T * n_used * 4, "indices") || !fits(scores, T * n_used * 4, "scores"))
+        return -1;
+    const WsFixed fx{ g.scratch_dev[g.device], kScratchBytes };
+    return moe_batch(fptr(input), nullptr, w_gate_inp, w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type,
+                     down_type, gate_row_stride, up_row_stride, down_row_stride, expert_offsets, fptr(output),
+                     residual ? fptr(residual) : nullptr, gate_logits ? fptr(gate_logits) : nullptr,
+                     indices ? (int32_t *)dptr(indices) : nullptr, scores ? fptr(scores) : nullptr, n_tokens, n_embd,
+                     n_expert, n_used, n_ff_exp, router_row_stride, router_type, norm_topk_prob,
+                     "moe_ffn_batch_noalloc", &fx);
+}
+
+extern "C" size_t ds3_hip_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
 // reference src/ds3_engine.c:519-527, 675-720 (rms_norm, zero, moe_ffn, vec_add around the MoE)
 extern "C" int ds3_hip_moe_block(

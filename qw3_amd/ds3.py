@@ -141,14 +141,18 @@ def moe_bucket(indices: Buffer, scores: Buffer, n_tokens: int, n_used: int, n_ex
 def moe_ffn_batch(x: Buffer, router: Buffer, router_type: int, ex: ExpertTensors, out: Buffer, n_tokens: int,
                   n_expert: int, n_used: int, residual: Buffer | None = None, logits: Buffer | None = None,
                   indices: Buffer | None = None, scores: Buffer | None = None, norm: bool = True,
-                  expert_offsets: Buffer | None = None) -> None:
+                  expert_offsets: Buffer | None = None, noalloc: bool = False) -> None:
+    """T tokens through the layer on the device (ds3_hip_moe_ffn_batch; with
+    noalloc, ds3_hip_moe_ffn_batch_noalloc: no allocation, intermediates in
+    the library's scratch array)."""
     gs, us, ds = ex.strides
-    _check(hip().ds3_hip_moe_ffn_batch(
+    fn = hip().ds3_hip_moe_ffn_batch_noalloc if noalloc else hip().ds3_hip_moe_ffn_batch
+    _check(fn(
         x, router, ex.gate, ex.up, ex.down,
         ex.gate_type, ex.up_type, ex.down_type, gs, us, ds, _h(expert_offsets),
         out, _h(residual), _h(logits), _h(indices), _h(scores),
         n_tokens, ex.n_embd, n_expert, n_used, ex.n_ff, row_bytes(router_type, ex.n_embd), router_type, norm),
-        "moe_ffn_batch")
+        "moe_ffn_batch_noalloc" if noalloc else "moe_ffn_batch")
 
 
 def moe_block(hidden: Buffer, ffn_norm: Buffer, eps: float, router: Buffer, router_type: int, ex: ExpertTensors,
