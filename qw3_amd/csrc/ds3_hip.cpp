@@ -1155,7 +1155,7 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
     const size_t T = n_tokens;
 
     const bool grouped_ok = gate_type == up_type && grouped_type_ok(gate_type, (int)n_embd) &&
-                            grouped_type_ok(down_type, (int)n_ff_exp) && n_ff_exp % 128 == 0 && n_embd % 128 == 0;
+                            grouped_type_ok(down_type, (int)n_ff_exp) && grouped_shape_ok((int)n_embd, (int)n_ff_exp);
     const bool use_grouped = grouped_ok && (int)n_tokens >= g.prefill_min;
     const int chunk = use_grouped ? prefill_chunk(n_expert) : (int)n_tokens;
     const size_t Tc = (size_t)(chunk < (int)n_tokens ? chunk : (int)n_tokens);
@@ -1168,8 +1168,10 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
     const RouteScratch rs = route_scratch((int)T, n_embd, n_expert);
     const size_t o_w = bp.take(rs.bytes);
     size_t o_h = 0, o_t = 0, o_x16 = 0, o_cnt = 0, o_off = 0, o_ids = 0, o_wts = 0, o_pos = 0, o_tiles = 0, o_nt = 0,
-           o_h16 = 0, o_y = 0;
+           o_h16 = 0, o_y = 0, o_rg = 0, o_rd = 0;
+    int rpi_gu = 0, rpi_dn = 0;
     if (use_grouped) {
+        grouped_runs_per_tile((int)n_embd, (int)n_ff_exp, rpi_gu, rpi_dn);
         o_x16 = bp.take(T * n_embd * 2);
         o_cnt = bp.take((size_t)n_expert * 4);
         o_off = bp.take(((size_t)n_expert + 1) * 4);
@@ -1177,7 +1179,9 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
         o_wts = bp.take(S * 4);
         o_pos = bp.take(S * 4);
         o_tiles = bp.take((size_t)max_tiles * 4);
-        o_nt = bp.take(4);
+        o_nt = bp.take(16);                          // n_tiles, then the two run counts
+        o_rg = bp.take((size_t)max_tiles * rpi_gu * 4);
+        o_rd = bp.take((size_t)max_tiles * rpi_dn * 4);
         o_h16 = bp.take(S * n_ff_exp * 2);
         o_y = bp.take(S * n_embd * 4);
     } else {
@@ -1234,7 +1238,8 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
         return finish(hipSuccess, what);
     }
     BucketOut bo{ (int32_t *)(ws + o_cnt), (int32_t *)(ws + o_off), (int32_t *)(ws + o_ids), (float *)(ws + o_wts),
-                  (int32_t *)(ws + o_pos), (int32_t *)(ws + o_tiles), (int32_t *)(ws + o_nt), max_tiles, 64 };
+                  (int32_t *)(ws + o_pos), (int32_t *)(ws + o_tiles), (int32_t *)(ws + o_nt), max_tiles, 64,
+                  (int32_t *)(ws + o_rg), (int32_t *)(ws + o_rd), (int32_t *)(ws + o_nt) + 1, rpi_gu, rpi_dn };
     _Float16 *x16_all = (_Float16 *)(ws + o_x16), *h16 = (_Float16 *)(ws + o_h16);
     float *y = (float *)(ws + o_y);
     if (!x16_done) {

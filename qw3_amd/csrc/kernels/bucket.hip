@@ -114,6 +114,23 @@ k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int 
         *o.n_tiles = total_t < o.max_tiles ? total_t : o.max_tiles;
     }
     __syncthreads();
+    if (o.runs_gu != nullptr) {
+        // run lists: (tile, n-run) for every tile, gate_up's and down's
+        int rg = e < E ? ntile * o.rpi_gu : 0, rd = e < E ? ntile * o.rpi_dn : 0;
+        int tg = 0, td = 0;
+        block_scan2(rg, rd, tg, td, E, wsum);
+        if (e < E) {
+            for (int m = 0; m < ntile && tb + m < o.max_tiles; m++) {
+                for (int j = 0; j < o.rpi_gu; j++) o.runs_gu[rg++] = ((tb + m) << 12) | j;
+                for (int j = 0; j < o.rpi_dn; j++) o.runs_dn[rd++] = ((tb + m) << 12) | j;
+            }
+        }
+        if (threadIdx.x == 0) {
+            o.n_runs[0] = tg;
+            o.n_runs[1] = td;
+        }
+    }
+    __syncthreads();
     auto place = [&](int s, int ex, float sc) {
         const int t = s / k;
         if (ex < 0 || ex >= E) {          // out-of-range id: the slot is dropped

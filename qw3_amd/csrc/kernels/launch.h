@@ -136,6 +136,12 @@ struct BucketOut {
     int32_t *n_tiles;    // [1]
     int max_tiles;
     int tile_m;
+    // Optional run lists of the grouped kernels (null: not written): runs
+    // (tile, n-run) packed tile << 12 | n_run, in tile order.
+    int32_t *runs_gu;    // [max_tiles * rpi_gu]
+    int32_t *runs_dn;    // [max_tiles * rpi_dn]
+    int32_t *n_runs;     // [2]: gate_up runs, down runs
+    int rpi_gu, rpi_dn;  // n-runs per token tile (n tiles / n tiles per run)
 };
 hipError_t launch_bucket(const int32_t *idx, const float *scores, int T, int k, int E,
                          const BucketOut &o, hipStream_t s);
@@ -147,6 +153,13 @@ hipError_t launch_grouped_gate_up(const _Float16 *x16, int K, const ExpertWeight
 hipError_t launch_grouped_down(const _Float16 *h16, int F, const ExpertWeights &ew, int N,
                                const BucketOut &b, float *y, hipStream_t s);
 bool grouped_type_ok(int type, int K);
+// Layer shapes the grouped kernels take: n_embd a multiple of 512 (gate_up's
+// activation chunks), n_ff a multiple of 128 and at most 1024 (down's token
+// tile stays in LDS).
+bool grouped_shape_ok(int n_embd, int n_ff);
+// n-runs per token tile of the grouped kernels for a layer shape (BucketOut
+// rpi_gu / rpi_dn).
+void grouped_runs_per_tile(int n_embd, int n_ff, int &rpi_gu, int &rpi_dn);
 
 // out[t][j] = (accumulate ? out : 0) + sum_k w[t][k] * y[slot_pos[t*k+kk]][j] (+ residual)
 hipError_t launch_combine(const float *y, const int32_t *slot_pos, const float *wts, int T, int k,
