@@ -276,9 +276,12 @@ struct DeferredSel {
 
 // Per-token expert products for `slots` routed slots of T tokens:
 // h = swiglu(gate, up) then out (+)= sum_k w_k * down(h_k).
+// With xt (tokens routed by the certified router's selection launch), the
+// gate/up launch also recomputes their weights from exact logits.
 int run_experts_decode(const float *x, int64_t ldx, const int32_t *idx, const float *wts, int T, int n_used,
                        const ExpertWeights &ew, uint32_t n_embd, uint32_t n_ff, float *out, const float *residual,
-                       bool accumulate, float *h, float *tmp_up, const DeferredSel *sel = nullptr)
+                       bool accumulate, float *h, float *tmp_up, const DeferredSel *sel = nullptr,
+                       const ExactTail *xt = nullptr)
 {
     const int slots = T * n_used;
     hipError_t e;
@@ -289,7 +292,7 @@ int run_experts_decode(const float *x, int64_t ldx, const int32_t *idx, const fl
         e = launch_decode_gate_up_sel(x, T, n_used, ew, (int)n_embd, (int)n_ff, h, sel->cs, sel->ra, g.stream);
     } else if (ew.gate_type == ew.up_type) {
         KScope ks("moe_decode_gate_up");
-        e = launch_decode_gate_up(x, ldx, idx, slots, n_used, ew, (int)n_embd, (int)n_ff, h, g.stream);
+        e = launch_decode_gate_up(x, ldx, idx, slots, n_used, ew, (int)n_embd, (int)n_ff, h, g.stream, xt);
     } else {
         // Mismatched gate/up types: two projections, then silu_mul
         // (the reference's unfused fallback, src/ds3_metal.m:2107-2140).
@@ -297,7 +300,7 @@ int run_experts_decode(const float *x, int64_t ldx, const int32_t *idx, const fl
         eg.up = ew.gate; eg.up_type = ew.gate_type; eg.up_stride = ew.gate_stride;
         eu.gate = ew.up; eu.gate_type = ew.up_type; eu.gate_stride = ew.up_stride;
         KScope ks("moe_decode_proj");
-        e = launch_decode_proj(x, ldx, idx, slots, n_used, eg, 0, (int)n_embd, (int)n_ff, h, g.stream);
+        e = launch_decode_proj(x, ldx, idx, slots, n_used, eg, 0, (int)n_embd, (int)n_ff, h, g.stream, xt);
         if (e == hipSuccess)
             e = launch_decode_proj(x, ldx, idx, slots, n_used, eu, 1, (int)n_embd, (int)n_ff, tmp_up, g.stream);
         if (e == hipSuccess) e = launch_silu_mul(h, tmp_up, h, (int64_t)slots * n_ff, g.stream);
@@ -780,11 +783,16 @@ bool use_cert(const float *x, int T, uint32_t n_embd, uint32_t n_expert, uint32_
 // the decode gate/up kernel (defer->on): the routing outputs are then written
 // by that kernel.  With np (certified router only), x holds raw rows and the
 // router's sums kernel normalises them, writing np->xn, which the rest of the
-// routing reads.
+// routing reads.  allow_cert: the caller runs the decode gate/up kernels next
+// and passes them `exact`, which is set (exact->w != nullptr) when the
+// certified selection launch routed the tokens: those kernels then replace
+// its weights with ones from the exact logits of the selected experts.
 int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstride, int rtype, int T, uint32_t n_embd,
                  uint32_t n_expert, uint32_t n_used, bool norm, const RouteBufs &rb, bool *x16_done = nullptr,
-                 bool allow_cert = false, DeferredSel *defer = nullptr, const NormPro *np = nullptr)
+                 bool allow_cert = false, DeferredSel *defer = nullptr, const NormPro *np = nullptr,
+                 ExactTail *exact = nullptr)
 {
+    if (exact) *exact = ExactTail{};
     RouteArgs ra{};
     ra.logits = rb.logits;
     ra.idx = rb.idx;
@@ -815,9 +823,16 @@ int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstrid
                 defer->ra = ra;
             }
         } else if (e == hipSuccess) {
-            KScope ks("router_select");
-            e = launch_router_cert(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, rb.wf32,
-                                   rb.logits, n_expert, rb.x16, ra, rb.cert, g.cert_stats, 2, g.stream);
+            {
+                KScope ks("router_select");
+                e = launch_router_cert(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, rb.wf32,
+                                       rb.logits, n_expert, rb.x16, ra, rb.cert, g.cert_stats, 2, g.stream);
+            }
+            CertSel cs{};
+            if (e == hipSuccess && exact != nullptr &&
+                router_cert_sel(T, (int)n_embd, (int)n_expert, (int)n_used, rtype, cptr(router), rstride, rb.wf32,
+                                rb.cert, g.cert_stats, 1, &cs) == hipSuccess)
+                *exact = ExactTail{ cs.w, cs.wstride, ra };
         }
         if (x16_done) *x16_done = rb.x16 != nullptr;
         return report(e, "router (certified)");
@@ -901,8 +916,9 @@ extern "C" int ds3_hip_moe_ffn(
     const float *x = fptr(input);
     const RouteBufs rb = route_bufs(ws + o_r, rs, fptr(gate_logits), idx, sc, nullptr);
     DeferredSel sel;
+    ExactTail xt{};
     if (route_tokens(x, w_gate_inp, router_row_stride, router_type, 1, n_embd, n_expert, n_used, norm_topk_prob,
-                     rb, nullptr, true, gate_type == up_type ? &sel : nullptr) != 0)
+                     rb, nullptr, true, gate_type == up_type ? &sel : nullptr, nullptr, &xt) != 0)
         return -1;
     if (has_shared &&
         run_shared(x, w_shared_gate, w_shared_up, w_shared_down, shared_gate_type, shared_up_type, shared_down_type,
@@ -912,7 +928,7 @@ extern "C" int ds3_hip_moe_ffn(
     ExpertWeights ew = make_ew(w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type, down_type, gate_row_stride,
                                up_row_stride, down_row_stride, expert_offsets);
     if (run_experts_decode(x, n_embd, idx, sc, 1, (int)n_used, ew, n_embd, n_ff_exp, fptr(output), nullptr, true, h,
-                           tmp, &sel) != 0)
+                           tmp, &sel, xt.w ? &xt : nullptr) != 0)
         return -1;
     return finish(hipSuccess, "moe_ffn");
 }
@@ -1212,7 +1228,7 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
     if (norm) {
         float *xn = norm->xn ? norm->xn : (float *)(ws + o_xn);
         np = NormPro{ norm->weight, norm->eps, xn };
-        fuse_norm = use_cert(x_in, (int)T, n_embd, n_expert, n_used, true) &&
+        fuse_norm = use_cert(x_in, (int)T, n_embd, n_expert, n_used, !use_grouped) &&
                     ((uintptr_t)norm->weight & 15) == 0 && ((uintptr_t)xn & 15) == 0;
         if (!fuse_norm) {
             KScope ks("rms_norm");
@@ -1222,18 +1238,21 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
             x = xn;
         }
     }
+    // the certified router only ahead of the decode kernels, which make its
+    // weights exact (ExactTail / the fused selection)
     bool x16_done = false;
     DeferredSel sel;
+    ExactTail xt{};
     if (route_tokens(x, w_gate_inp, router_row_stride, router_type, (int)T, n_embd, n_expert, n_used, norm_topk_prob,
-                     rb, &x16_done, true, !use_grouped && gate_type == up_type ? &sel : nullptr,
-                     fuse_norm ? &np : nullptr) != 0)
+                     rb, &x16_done, !use_grouped, !use_grouped && gate_type == up_type ? &sel : nullptr,
+                     fuse_norm ? &np : nullptr, &xt) != 0)
         return -1;
     if (fuse_norm) x = np.xn;
     ExpertWeights ew = make_ew(w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type, down_type, gate_row_stride,
                                up_row_stride, down_row_stride, expert_offsets);
     if (!use_grouped) {
         if (run_experts_decode(x, n_embd, rb.idx, rb.scores, (int)T, (int)n_used, ew, n_embd, n_ff_exp, out, res, true,
-                               (float *)(ws + o_h), (float *)(ws + o_t), &sel) != 0)
+                               (float *)(ws + o_h), (float *)(ws + o_t), &sel, xt.w ? &xt : nullptr) != 0)
             return -1;
         return finish(hipSuccess, what);
     }

@@ -104,21 +104,36 @@ struct CertSel {
 hipError_t router_cert_sel(int T, int K, int E, int k, int rtype, const uint8_t *rw, uint64_t rstride, float *wf32,
                            void *scratch, unsigned long long *stats, int nb, CertSel *out);
 
+// Weights of tokens routed by the certified router (k_router_select) from
+// the exact logits of their selected experts, computed by a column of
+// workgroups appended to the decode gate/up launch: w = the FP32 router rows
+// the selection used, ra = the routing (idx / scores rows of n_used entries,
+// the logits rows, whose selected entries become exact).
+struct ExactTail {
+    const float *w;
+    int64_t wstride;
+    RouteArgs ra;
+};
+
 // Decode (small T) expert products.
 //   h[slot][F] = silu(x[t] . Wg_e) * (x[t] . Wu_e), slot = t*n_used + k, e = idx[slot]
+// With xt, also the exact weights of the tokens (xt->ra.idx == idx).
 hipError_t launch_decode_gate_up(const float *x, int64_t ldx, const int32_t *idx, int n_slots,
                                  int n_used, const ExpertWeights &ew, int K, int F,
-                                 float *h, hipStream_t s);
+                                 float *h, hipStream_t s, const ExactTail *xt = nullptr);
 // The same for the T tokens of x (rows K floats apart), with the expert of
 // each slot chosen in the kernel by the certified router's selection over
 // cs (launch_router_cert phase 1 done); writes ra.idx / ra.scores (and
-// repaired logits) as the selection launch would.
+// repaired logits) as the selection launch would, the weights of certified
+// tokens from the exact logits of their selected experts (which replace
+// those entries of the logits rows).
 hipError_t launch_decode_gate_up_sel(const float *x, int T, int n_used, const ExpertWeights &ew, int K, int F,
                                      float *h, const CertSel &cs, const RouteArgs &ra, hipStream_t s);
 //   out[slot][F] = x[t] . W_e with W = ew.gate / gate_type / gate_stride and
 //   expert offsets from table column `which` (0 gate, 1 up).
 hipError_t launch_decode_proj(const float *x, int64_t ldx, const int32_t *idx, int n_slots, int n_used,
-                              const ExpertWeights &ew, int which, int K, int F, float *out, hipStream_t s);
+                              const ExpertWeights &ew, int which, int K, int F, float *out, hipStream_t s,
+                              const ExactTail *xt = nullptr);
 //   out[t][j] (+)= sum_k w[t][k] * (h[slot] . Wd_e[j]) in k order
 hipError_t launch_decode_down(const float *h, const int32_t *idx, const float *wts, int T,
                               int n_used, const ExpertWeights &ew, int K, int F,

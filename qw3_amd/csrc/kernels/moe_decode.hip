@@ -18,6 +18,7 @@ __device__ __forceinline__ const uint8_t *expert_base(const uint8_t *base, const
 }
 
 constexpr int DEC_TPB = 256;
+static_assert(DEC_TPB == XC_THREADS, "the exact-weights stage runs on a decode workgroup's four waves");
 #ifndef DS3_DOWN_PREFETCH
 #define DS3_DOWN_PREFETCH 1    // T = 1: the fused gate/up kernel warms L2 with the down rows
 #endif
@@ -35,17 +36,17 @@ constexpr int N_XCD_DEC = 8;   // MI355X: workgroups go round-robin to 8 XCDs
 // group: the trip counts are compile-time and rows past F are clamped (their
 // results dropped), so every load of a wave is issued before its first dot
 // product and the wave pays one memory round trip.  Rows of expert e for
-// routed slot `slot` (token row xt).
+// routed slot `slot` (token row xt), row block rb of the expert.
 template <int GT, int G, int UPL, bool PAIR, int RPW = 2>
-__device__ __forceinline__ void gate_up_rows(const float *__restrict__ xt, int slot, int e, const ExpertWeights &ew,
-                                             int K, int F, int which, float *__restrict__ h)
+__device__ __forceinline__ void gate_up_rows(const float *__restrict__ xt, int slot, int rb, int e,
+                                             const ExpertWeights &ew, int K, int F, int which, float *__restrict__ h)
 {
     constexpr int GPW = WAVE / G;
     const uint8_t *wg = expert_base(ew.gate, ew.table, e, PAIR ? 0 : which, (uint64_t)F, ew.gate_stride);
     const uint8_t *wu = PAIR ? expert_base(ew.up, ew.table, e, 1, (uint64_t)F, ew.up_stride) : wg;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     const int gl = lane % G, grp = lane / G;
-    const int r0 = (blockIdx.x * (DEC_TPB / WAVE) + wave) * GPW * RPW + grp;
+    const int r0 = (rb * (DEC_TPB / WAVE) + wave) * GPW * RPW + grp;
     float ag[RPW], au[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
@@ -74,48 +75,44 @@ __device__ __forceinline__ void gate_up_rows(const float *__restrict__ xt, int s
     }
 }
 
+// One-dimensional grid: n_exact workgroups first (xt.w set: workgroup t
+// recomputes token t's weights from the exact logits of its selected
+// experts, exact_weights_wg, routing by k_router_select; dispatched first,
+// they run beside the row workgroups), then nx row blocks per slot.
 template <int GT, int G, int UPL, bool PAIR>
 __global__ void __launch_bounds__(DEC_TPB)
 k_decode_gate_up(const float *__restrict__ x, int64_t ldx, const int32_t *__restrict__ idx, int n_used,
-                 ExpertWeights ew, int K, int F, int which, float *__restrict__ h)
+                 ExpertWeights ew, int K, int F, int which, float *__restrict__ h, int nx, int n_exact, ExactTail xt)
 {
-    const int slot = blockIdx.y;
-    gate_up_rows<GT, G, UPL, PAIR>(x + (int64_t)(slot / n_used) * ldx, slot, idx[slot], ew, K, F, which, h);
+    extern __shared__ __attribute__((aligned(16))) float xt_lds[];   // exact_chain_lds(K) bytes with xt.w set
+    if ((int)blockIdx.x < n_exact) {
+        const int t = blockIdx.x, wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
+        float4 xv[4];
+        exact_load_x(x + (int64_t)t * ldx, K, xv, threadIdx.x);
+        const int e_lane = lane < n_used ? idx[t * n_used + lane] : 0;
+        exact_store_x(xt_lds, K, xv, threadIdx.x);
+        __syncthreads();                                         // the row is in LDS
+        exact_weights_wg(xt_lds, K, xt.w, xt.wstride, xt.ra, t, e_lane, wave, lane);
+        return;
+    }
+    const int r = blockIdx.x - n_exact, slot = r / nx;
+    gate_up_rows<GT, G, UPL, PAIR>(x + (int64_t)(slot / n_used) * ldx, slot, r - slot * nx, idx[slot], ew, K, F,
+                                   which, h);
 }
 
-// gate_up with the certified router's selection in its prologue: every
-// wave ranks the experts of its token from the sums S / bounds B on its own
-// (no LDS, no barrier on the common path) and takes the expert of its slot;
-// a token it cannot certify is repaired by the whole workgroup.  Wave 0 of
-// workgroup x = 0 of each token's first slot also writes the token's
-// indices, weights (and repaired logits) for the down kernel and the caller,
-// after its products (a certified token's weights are not on their path).
-// This removes the selection launch and its memory round trip from the
-// decode chain.
-template <int GT, int G, int UPL>
-__global__ void __launch_bounds__(DEC_TPB)
-k_decode_gate_up_sel(const float *__restrict__ x, int n_used, ExpertWeights ew, int K, int F,
-                     float *__restrict__ h, CertSel cs, RouteArgs ra)
+// Warm each XCD's L2 with the down rows its down workgroups will read:
+// workgroups go round-robin to the 8 XCDs in dispatch order, so down
+// workgroup x (rows 8x .. 8x+7 of every selected expert, one token) runs on
+// XCD x % 8, as does gate/up workgroup `lin` (its linear index in a grid of
+// nwg).  One dword per 64-byte line; the values are only consumed, never
+// stored.  Whole 16-byte aligned 8-row blocks: every dword read lies inside
+// them.  e_rank: lane r < n_used holds the expert of rank r.
+__device__ __forceinline__ uint32_t prefetch_down_rows(const ExpertWeights &ew, int K, int n_used, int e_rank,
+                                                       int lin, int nwg)
 {
-    extern __shared__ __attribute__((aligned(16))) float sel_prod[];
-    const int slot = blockIdx.y, t = slot / n_used, kk = slot - t * n_used;
-    const int wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
-    const bool emit = blockIdx.x == 0 && kk == 0;
-    int e_rank = 0;
-    const bool ok = cert_select_wave(cs.ca, ra, t, false, lane, e_rank);
-    const bool certified = !__syncthreads_or(ok ? 0 : 1);   // pooled: the general path needs every wave
-    const int e = certified ? __builtin_amdgcn_readlane(e_rank, kk)
-                            : cert_select_tokens<1>(x, K, cs.w, cs.wstride, cs.ca, ra, t, emit, sel_prod)[kk];
-    // Warm each XCD's L2 with the down rows its down workgroups will read:
-    // workgroups go round-robin to the 8 XCDs in dispatch order, so down
-    // workgroup x (rows 8x .. 8x+7 of every selected expert, one token) runs
-    // on XCD x % 8, as does this workgroup's linear index.  One dword per
-    // 64-byte line; the values are only consumed, never stored.
     uint32_t pf = 0u;
-    // (whole 16-byte aligned 8-row blocks: every dword read lies inside them)
-    if (DS3_DOWN_PREFETCH && certified && n_used <= WAVE && K % 8 == 0 && ew.table == nullptr &&
+    if (DS3_DOWN_PREFETCH && n_used <= WAVE && K % 8 == 0 && ew.table == nullptr &&
         (8 * ew.down_stride) % 16 == 0 && ((uintptr_t)ew.down & 15) == 0) {
-        const int nx = gridDim.x, lin = blockIdx.y * nx + blockIdx.x, nwg = nx * gridDim.y;
         const int xcd = lin % N_XCD_DEC, li = lin / N_XCD_DEC, nli = (nwg - xcd + N_XCD_DEC - 1) / N_XCD_DEC;
         const int K_rows = K, dwg = K_rows / 8;                // down: n_embd rows, 8 per workgroup
         const int pairs = (dwg - xcd + N_XCD_DEC - 1) / N_XCD_DEC * n_used;
@@ -128,8 +125,53 @@ k_decode_gate_up_sel(const float *__restrict__ x, int n_used, ExpertWeights ew, 
             for (int l = threadIdx.x; l < lines; l += DEC_TPB) pf ^= *(const uint32_t *)(base + 64 * (size_t)l);
         }
     }
-    gate_up_rows<GT, G, UPL, true, DS3_SEL_RPW>(x + (int64_t)t * K, slot, e, ew, K, F, 0, h);
-    if (certified && emit && wave == 0) cert_emit_any(cs.ca, ra, t, lane, e_rank);
+    return pf;
+}
+
+// gate_up with the certified router's selection in its prologue: every
+// wave ranks the experts of its token from the sums S / bounds B on its own
+// (no LDS, no barrier on the common path) and takes the expert of its slot;
+// a token it cannot certify is repaired by the whole workgroup, and wave 0
+// of the token's first row block writes its routing outputs.  A certified
+// token's outputs come from its exact-weights workgroup (the first T of the
+// one-dimensional grid, dispatched first): it evaluates the reference's
+// exact logits of the k selected experts and the weights from them
+// (exact_weights_wg) while the row workgroups (nx per slot) stream the
+// expert weights.  This removes the selection launch and its memory round
+// trip from the decode chain.
+template <int GT, int G, int UPL>
+__global__ void __launch_bounds__(DEC_TPB)
+k_decode_gate_up_sel(const float *__restrict__ x, int n_used, ExpertWeights ew, int K, int F,
+                     float *__restrict__ h, int nx, CertSel cs, RouteArgs ra)
+{
+    extern __shared__ __attribute__((aligned(16))) float sel_prod[];
+    const int wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
+    const int lin = blockIdx.x, nwg = gridDim.x;
+    int e_rank = 0;
+    if ((int)blockIdx.x < ra.T) {
+        const int t = blockIdx.x;
+        // every wave ranks the token (the same result: an uncertified token,
+        // left to the repair, leaves the whole workgroup) and stages a part
+        // of its row
+        float4 xv[4];
+        exact_load_x(x + (int64_t)t * K, K, xv, threadIdx.x);
+        const bool ok = cert_select_wave(cs.ca, ra, t, false, lane, e_rank);
+        if (!ok) return;
+        exact_store_x(sel_prod, K, xv, threadIdx.x);
+        __syncthreads();                                         // the row is in LDS
+        exact_weights_wg(sel_prod, K, cs.w, cs.wstride, ra, t, e_rank, wave, lane);
+        if (wave == 0 && lane == 0 && cs.ca.stats != nullptr) atomicAdd(&cs.ca.stats[0], 1ull);
+        return;
+    }
+    const int r = blockIdx.x - ra.T, slot = r / nx, rb = r - slot * nx;
+    const int t = slot / n_used, kk = slot - t * n_used;
+    const bool ok = cert_select_wave(cs.ca, ra, t, false, lane, e_rank);
+    const bool emit = rb == 0 && kk == 0;
+    const bool certified = !__syncthreads_or(ok ? 0 : 1);   // pooled: the general path needs every wave
+    const int e = certified ? __builtin_amdgcn_readlane(e_rank, kk)
+                            : cert_select_tokens<1>(x, K, cs.w, cs.wstride, cs.ca, ra, t, emit, sel_prod)[kk];
+    const uint32_t pf = certified ? prefetch_down_rows(ew, K, n_used, e_rank, lin, nwg) : 0u;
+    gate_up_rows<GT, G, UPL, true, DS3_SEL_RPW>(x + (int64_t)t * K, slot, rb, e, ew, K, F, 0, h);
     asm volatile("" ::"v"(pf));                // the prefetch loads stay
 }
 
@@ -321,29 +363,44 @@ static int lanes_per_row(int units)
     }
 
 
+static bool exact_tail_ok(const ExactTail *xt, int n_slots, int n_used, int K)
+{
+    return xt->ra.k == n_used && xt->ra.T * n_used == n_slots && xt->ra.idx != nullptr && xt->ra.scores != nullptr &&
+           xt->ra.logits != nullptr && xt->ra.out_stride == n_used && router_cert_ok(K, xt->ra.E, n_used) &&
+           ((uintptr_t)xt->w & 15) == 0 && xt->wstride % 4 == 0;
+}
+
 static hipError_t decode_gate_up_impl(const float *x, int64_t ldx, const int32_t *idx, int n_slots, int n_used,
                                       const ExpertWeights &ew, int K, int F, float *h, bool pair, int which,
-                                      hipStream_t s)
+                                      const ExactTail *xt, hipStream_t s)
 {
     if (!gemv_type_ok(ew.gate_type, K) || n_slots <= 0 || F <= 0) return hipErrorInvalidValue;
+    if (xt != nullptr && (!exact_tail_ok(xt, n_slots, n_used, K) || idx != xt->ra.idx || ldx % 4 != 0 ||
+                          ((uintptr_t)x & 15) != 0))
+        return hipErrorInvalidValue;
+    const ExactTail tail = xt != nullptr ? *xt : ExactTail{};
+    const size_t lds = xt != nullptr ? exact_chain_lds(K) : 0;
     const int G = lanes_per_row(K / 32), UPL = K / 32 / G;
     const int rows_per_wg = (DEC_TPB / WAVE) * (WAVE / G) * 2;     // 2 rows per lane group
-    const dim3 grid((unsigned)((F + rows_per_wg - 1) / rows_per_wg), (unsigned)n_slots);
+    const int nx = (F + rows_per_wg - 1) / rows_per_wg, n_exact = xt != nullptr ? xt->ra.T : 0;
+    const dim3 grid((unsigned)(n_exact + (int64_t)nx * n_slots));
     if (pair) {
         DS3_T_SWITCH(ew.gate_type, DS3_G_SWITCH(G, DS3_U_SWITCH(UPL, hipLaunchKernelGGL(
-            (k_decode_gate_up<TV, GV, UV, true>), grid, dim3(DEC_TPB), 0, s, x, ldx, idx, n_used, ew, K, F, which, h))));
+            (k_decode_gate_up<TV, GV, UV, true>), grid, dim3(DEC_TPB), lds, s, x, ldx, idx, n_used, ew, K, F, which, h,
+            nx, n_exact, tail))));
     } else {
         DS3_T_SWITCH(ew.gate_type, DS3_G_SWITCH(G, DS3_U_SWITCH(UPL, hipLaunchKernelGGL(
-            (k_decode_gate_up<TV, GV, UV, false>), grid, dim3(DEC_TPB), 0, s, x, ldx, idx, n_used, ew, K, F, which, h))));
+            (k_decode_gate_up<TV, GV, UV, false>), grid, dim3(DEC_TPB), lds, s, x, ldx, idx, n_used, ew, K, F, which, h,
+            nx, n_exact, tail))));
     }
     return hipGetLastError();
 }
 
 hipError_t launch_decode_gate_up(const float *x, int64_t ldx, const int32_t *idx, int n_slots, int n_used,
-                                 const ExpertWeights &ew, int K, int F, float *h, hipStream_t s)
+                                 const ExpertWeights &ew, int K, int F, float *h, hipStream_t s, const ExactTail *xt)
 {
     if (ew.gate_type != ew.up_type) return hipErrorInvalidValue;
-    return decode_gate_up_impl(x, ldx, idx, n_slots, n_used, ew, K, F, h, true, 0, s);
+    return decode_gate_up_impl(x, ldx, idx, n_slots, n_used, ew, K, F, h, true, 0, xt, s);
 }
 
 hipError_t launch_decode_gate_up_sel(const float *x, int T, int n_used, const ExpertWeights &ew, int K, int F,
@@ -354,17 +411,23 @@ hipError_t launch_decode_gate_up_sel(const float *x, int T, int n_used, const Ex
         return hipErrorInvalidValue;
     const int G = lanes_per_row(K / 32), UPL = K / 32 / G;
     const int rows_per_wg = (DEC_TPB / WAVE) * (WAVE / G) * DS3_SEL_RPW;
-    const dim3 grid((unsigned)((F + rows_per_wg - 1) / rows_per_wg), (unsigned)(T * n_used));
-    const size_t lds = (size_t)cs.ca.nb * (K + 4) * sizeof(float);
+    if (((uintptr_t)x & 15) != 0 || ((uintptr_t)cs.w & 15) != 0 || cs.wstride % 4 != 0 || ra.out_stride != n_used ||
+        ra.logits == nullptr)
+        return hipErrorInvalidValue;
+    // T exact-weights workgroups, then nx row blocks per slot
+    const int nx = (F + rows_per_wg - 1) / rows_per_wg;
+    const dim3 grid((unsigned)(T + (int64_t)nx * T * n_used));
+    const size_t lds = std::max((size_t)cs.ca.nb * (K + 4) * sizeof(float), exact_chain_lds(K));
     DS3_T_SWITCH(ew.gate_type, DS3_G_SWITCH(G, DS3_U_SWITCH(UPL, hipLaunchKernelGGL(
-        (k_decode_gate_up_sel<TV, GV, UV>), grid, dim3(DEC_TPB), lds, s, x, n_used, ew, K, F, h, cs, ra))));
+        (k_decode_gate_up_sel<TV, GV, UV>), grid, dim3(DEC_TPB), lds, s, x, n_used, ew, K, F, h, nx, cs, ra))));
     return hipGetLastError();
 }
 
 hipError_t launch_decode_proj(const float *x, int64_t ldx, const int32_t *idx, int n_slots, int n_used,
-                              const ExpertWeights &ew, int which, int K, int F, float *out, hipStream_t s)
+                              const ExpertWeights &ew, int which, int K, int F, float *out, hipStream_t s,
+                              const ExactTail *xt)
 {
-    return decode_gate_up_impl(x, ldx, idx, n_slots, n_used, ew, K, F, out, false, which, s);
+    return decode_gate_up_impl(x, ldx, idx, n_slots, n_used, ew, K, F, out, false, which, xt, s);
 }
 
 hipError_t launch_decode_down(const float *h, const int32_t *idx, const float *wts, int T, int n_used,

@@ -575,6 +575,220 @@ __device__ inline bool cert_select_wave(const CertArgs &ca, const RouteArgs &a, 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Exact weights of a routed token.  A certified token's top k is the
+// reference's, but fl32(S) is not its logit: the reference's chain rounds
+// ~K times and lands up to B away, and the softmax carries that into the
+// weights (~1e-5 relative at |logit| ~ 10).  So the selected experts' logits
+// are recomputed as the reference's exact chains and the weights derived
+// from them, off the critical path: a workgroup appended to the decode
+// gate/up grid does it while the other workgroups stream the expert rows.
+// ---------------------------------------------------------------------------
+
+// One chain step for block (wq, xq) (elements 32 b + 4 j + c of lane 8 m + j):
+// lane 8 m adds, in order, the four products of each lane 8 m + JJ, JJ =
+// 0 .. 7, taking them through DPP row_shl:JJ (lane 8 m and 8 m + 7 share a
+// row of 16 lanes).
+template <int JJ>
+__device__ __forceinline__ float chain_from_lane(float acc, const float (&q)[4])
+{
+#pragma clang fp contract(off)
+    if constexpr (JJ == 0) {
+        acc = acc + q[0];
+        acc = acc + q[1];
+        acc = acc + q[2];
+        acc = acc + q[3];
+    } else {
+        acc = acc + dpp_f<0x100 + JJ>(q[0]);
+        acc = acc + dpp_f<0x100 + JJ>(q[1]);
+        acc = acc + dpp_f<0x100 + JJ>(q[2]);
+        acc = acc + dpp_f<0x100 + JJ>(q[3]);
+    }
+    return acc;
+}
+
+__device__ __forceinline__ float chain_block(float acc, const float4 &wq, const float4 &xq)
+{
+#pragma clang fp contract(off)
+    const float q[4] = { xq.x * wq.x, xq.y * wq.y, xq.z * wq.z, xq.w * wq.w };   // the reference's rounded products
+    acc = chain_from_lane<0>(acc, q);
+    acc = chain_from_lane<1>(acc, q);
+    acc = chain_from_lane<2>(acc, q);
+    acc = chain_from_lane<3>(acc, q);
+    acc = chain_from_lane<4>(acc, q);
+    acc = chain_from_lane<5>(acc, q);
+    acc = chain_from_lane<6>(acc, q);
+    return chain_from_lane<7>(acc, q);
+}
+
+// The exact chain is 2048 dependent fp32 additions per logit at K = 2048:
+// ~4.5 cycles each, and any other instruction of the adding wave costs its
+// issue slot on top (a DPP operand also stalls a dependent add by 2 wait
+// states).  So the work is split: waves 1-3 (producers) stream the router
+// rows of the selected experts into LDS by DMA, multiply them by the token's
+// row and write the products transposed, block by block (a block = 32
+// consecutive elements of each of 8 experts); wave 0 (the consumer) reads
+// each expert's 32 products in order with 8 LDS reads and adds them.  One
+// workgroup barrier per chunk of XC_CH blocks hands a product buffer over.
+constexpr int XC_CH = 4;        // blocks per chunk
+constexpr int XC_PS = 36;       // floats per expert in a block's products: 32 + 4 (conflict-free reads)
+constexpr int XC_NP = 3;        // producer waves
+constexpr int XC_RP = 7;        // DMA ring slots (1 KiB blocks) per producer wave: ~1.4 us of lookahead
+constexpr int XC_THREADS = (XC_NP + 1) * WAVE;
+
+// LDS of the exact stage: the token's row (K floats), two product buffers,
+// the producers' DMA rings.
+__host__ __device__ constexpr size_t exact_chain_lds(int K)
+{
+    return (size_t)K * 4 + (size_t)2 * XC_CH * 8 * XC_PS * 4 + (size_t)XC_NP * XC_RP * 1024;
+}
+
+// One 16-byte DMA per lane from src into LDS at lds_base + 16 * lane
+// (global_load_lds_dwordx4, LDS base in M0, which the statement restores).
+// Issued outside the compiler's view, so that it neither waits for the ring
+// before every LDS access nor counts it: the caller's explicit vmcnt waits
+// order it.  Waits for this wave's earlier LDS reads first (a slot is
+// rewritten only after it was read).
+__device__ __forceinline__ void chain_dma(const float *src, uint32_t lds_base)
+{
+    uint32_t m0_save;
+    asm volatile("s_waitcnt lgkmcnt(0)\n\t"
+                 "s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %2\n\t"
+                 "global_load_lds_dwordx4 %1, off\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(m0_save)
+                 : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_base))   // wave-uniform: in an SGPR
+                 : "memory");
+}
+
+// The token's row into LDS (lds[0 .. K), K <= 4096) by the XC_THREADS
+// threads of the workgroup, in two steps, so that other loads (the
+// selection's) can be in flight between them.
+__device__ __forceinline__ void exact_load_x(const float *__restrict__ xrow, int K, float4 (&xv)[4], int tid)
+{
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int i = 4 * (tid + XC_THREADS * q);
+        if (i < K) xv[q] = *(const float4 *)(xrow + i);
+    }
+}
+
+__device__ __forceinline__ void exact_store_x(float *lds, int K, const float4 (&xv)[4], int tid)
+{
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int i = 4 * (tid + XC_THREADS * q);
+        if (i < K) *(float4 *)(lds + i) = xv[q];
+    }
+}
+
+// The reference's logits of the experts in lanes 0 .. k-1 of e_lane (every
+// wave holds them), exactly: acc = acc + x_i * w_i, i ascending, every
+// product and sum rounded to fp32 (src/ds3_reference.c:424-434).  Called by
+// all XC_THREADS threads of the workgroup (barriers inside) with the token's
+// row staged at lds[0 .. K) and visible; lds: exact_chain_lds(K) bytes.
+// Producer wave pw (wave pw + 1) owns blocks pw, pw + 3, ... and keeps XC_RP
+// of them in flight.  8 experts per pass (lane 8 m + j of a producer
+// multiplies elements 32 b + 4 j .. + 3 of expert m).  Wave 0, lane r < k,
+// returns e_r's logit.  K % 256 == 0.
+__device__ inline float exact_chain_wg(float *lds, int K, const float *__restrict__ w, int64_t wstride, int e_lane,
+                                       int k, int wave, int lane)
+{
+#pragma clang fp contract(off)
+    typedef __attribute__((address_space(3))) void lds_void;
+    const float *xs = lds;
+    float *pb = lds + K;                                    // [2][XC_CH][8][XC_PS]
+    const int nb = K / 32, nch = nb / XC_CH, m = lane >> 3, j = lane & 7, pw = wave - 1;
+    const float *wring = pb + 2 * XC_CH * 8 * XC_PS + max(pw, 0) * XC_RP * 256;   // this producer's DMA ring
+    const uint32_t ring = (uint32_t)(uintptr_t)(lds_void *)wring;
+    float res = 0.f;
+    for (int p0 = 0; p0 < k; p0 += 8) {
+        const float *wr = nullptr;
+        int slot = 0;
+        if (wave > 0) {
+            const int e = __shfl(e_lane, min(p0 + m, k - 1), WAVE);
+            wr = w + (int64_t)e * wstride + 4 * j;
+            for (int q = 0; q < XC_RP; q++) chain_dma(wr + 32 * min(pw + XC_NP * q, nb - 1), ring + 1024u * q);
+        }
+        float acc = 0.f;
+        for (int c = -1; c < nch; c++) {
+            if (wave > 0) {
+                const int cp = c + 1;                           // the chunk this round produces
+                if (cp < nch) {
+                    for (int b = cp * XC_CH; b < cp * XC_CH + XC_CH; b++) {
+                        if (b % XC_NP != pw) continue;          // uniform over the wave
+                        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(XC_RP - 1) : "memory");   // block b landed
+                        const float4 wq = *(const float4 *)(wring + 256 * slot + 4 * lane);
+                        const float4 xq = *(const float4 *)(xs + 32 * b + 4 * j);
+                        const float4 pq = make_float4(xq.x * wq.x, xq.y * wq.y, xq.z * wq.z, xq.w * wq.w);
+                        *(float4 *)(pb + (((cp & 1) * XC_CH + b % XC_CH) * 8 + m) * XC_PS + 4 * j) = pq;
+                        chain_dma(wr + 32 * min(b + XC_NP * XC_RP, nb - 1), ring + 1024u * slot);   // past the end: unused
+                        slot = slot + 1 == XC_RP ? 0 : slot + 1;
+                    }
+                }
+            } else if (c >= 0) {
+                // block bb + 1's products are read while block bb's are added
+                const float *pc = pb + ((c & 1) * XC_CH * 8 + m) * XC_PS;
+                float4 v[2][8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[0][i] = *(const float4 *)(pc + 4 * i);
+#pragma unroll
+                for (int bb = 0; bb < XC_CH; bb++) {
+                    if (bb + 1 < XC_CH) {
+#pragma unroll
+                        for (int i = 0; i < 8; i++) v[(bb + 1) & 1][i] = *(const float4 *)(pc + (bb + 1) * 8 * XC_PS + 4 * i);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        acc = acc + v[bb & 1][i].x;
+                        acc = acc + v[bb & 1][i].y;
+                        acc = acc + v[bb & 1][i].z;
+                        acc = acc + v[bb & 1][i].w;
+                    }
+                }
+            }
+            __syncthreads();                                    // chunk c consumed, chunk c + 1 written
+        }
+        if (wave > 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the ring drains before the next pass
+        const float v = __shfl(acc, 8 * min(max(lane - p0, 0), 7), WAVE);
+        if (lane >= p0 && lane < p0 + 8) res = v;
+    }
+    return res;
+}
+
+// Token t's routing outputs from the exact logits of its selected experts
+// (every wave: lane r < k of e_lane = the expert of rank r, already the
+// reference's order): the logits row supplies the other experts' values
+// (fl32(S), or exact chains where a repair computed them), the selected
+// entries are overwritten with their exact logits, and emit_ranked writes
+// idx / scores (wave 0).  All XC_THREADS threads of the workgroup call it,
+// with the token's row staged at lds[0 .. K) and visible.
+__device__ inline void exact_weights_wg(float *lds, int K, const float *__restrict__ w, int64_t wstride,
+                                        const RouteArgs &a, int t, int e_lane, int wave, int lane)
+{
+    float *lrow = (float *)a.logits + (int64_t)t * a.logit_stride;
+    float l[ROUTE_EPL];
+    if (wave == 0) {
+#pragma unroll
+        for (int jj = 0; jj < ROUTE_EPL; jj++) {            // lands during the chain
+            const int e = lane + WAVE * jj;
+            l[jj] = e < a.E ? lrow[e] : -INFINITY;
+        }
+    }
+    const float v = exact_chain_wg(lds, K, w, wstride, e_lane, a.k, wave, lane);
+    if (wave != 0) return;
+    for (int r = 0; r < a.k; r++) {
+        const int er = __builtin_amdgcn_readlane(e_lane, r);
+        const float vr = readlane_f(v, r);
+#pragma unroll
+        for (int jj = 0; jj < ROUTE_EPL; jj++)
+            if (lane + WAVE * jj == er) l[jj] = vr;
+    }
+    if (lane < a.k) lrow[e_lane] = v;
+    emit_ranked(a, t, l, lane < a.k ? v : 0.f, readlane_f(v, 0), e_lane, lane);
+}
+
 // Rank, certify and, where needed, repair the routing of tokens t0 ..
 // t0 + TG - 1 with the whole workgroup (RC_THREADS threads, all of which call
 // it).  Returns the LDS array [TG][WAVE] whose entries 0 .. k-1 of row tt are

@@ -449,6 +449,51 @@ def test_decode_near_ties_fused_select(hip_ready, real, T):
         assert_close(o1.read(np.float32, (1, 2048)), want, rel_l2=5e-5)
 
 
+@pytest.fixture(scope="module")
+def wide_router():
+    """Q4_K/Q6_K layer (n_ff 256) whose F32 router rows and inputs are
+    U(-0.5, 0.5), as in the reference's tests/test_moe_metal.c:148-156:
+    logits ~ N(0, 3.8), so the reference's chain lands ~1e-5 from the exact
+    sum and weights from fl32(S) would be ~1e-5 off."""
+    spec = W.LayerSpec(n_ff=256)
+    router = W.fill(W.UNIFORM, 31, 1, spec.n_expert * spec.n_embd, -0.5, 0.5).reshape(spec.n_expert, spec.n_embd)
+    print("  building wide-router layer", flush=True)
+    return Case(spec, seed=3131, router=router)
+
+
+@pytest.mark.parametrize("T", [1, 2, 12])
+def test_certified_weights_from_exact_logits(hip_ready, wide_router, T):
+    """Certified decode routing (T = 1 fused selection, T = 2 .. 12 the
+    selection launch): indices the reference's, the selected experts' logits
+    bit for bit the reference's sequential chains, and the weights those
+    logits give (within the device expf / division roundings)."""
+    case, s = wide_router, wide_router.spec
+    x = W.fill(W.UNIFORM, 40 + T, 2, T * s.n_embd, -0.5, 0.5).reshape(T, s.n_embd)
+    oi, osc, _, ol = oracle_route(case.wr, x, with_logits=True)
+    ds3.router_stats(reset=True)
+    print(f"  certified weights T={T}", flush=True)
+    got, gi, gs, gl = case.gpu_batch(x)
+    certified, repaired = ds3.router_stats()
+    print(f"    router: {certified} certified, {repaired} repaired", flush=True)
+    assert certified + repaired == T and certified >= T - 2      # a close pair may still send a token to repair
+    assert np.array_equal(gi, oi)
+    sel = np.take_along_axis(gl, gi, axis=1)
+    assert logit_bits_differ(sel, np.take_along_axis(ol, oi, axis=1)) == 0
+    rel = np.abs(gs - osc) / osc
+    print(f"    weights: max rel diff {rel.max():.2e}", flush=True)
+    assert rel.max() < 2e-6
+    want, _, _, _ = case.oracle(x)
+    assert_close(got, want, rel_l2=5e-5)
+    if T == 1:                                       # the single-token entry point
+        o1, l1 = ds3.Buffer.alloc(s.n_embd * 4), ds3.Buffer.alloc(s.n_expert * 4)
+        o1.zero()
+        ds3.moe_ffn(ds3.Buffer.from_array(x), case.dev.router, ds3.TYPE_F32, case.dev.experts, o1, l1, s.n_expert,
+                    W.N_USED)
+        l1h = l1.read(np.float32, (1, s.n_expert))
+        assert logit_bits_differ(np.take_along_axis(l1h, oi, axis=1), np.take_along_axis(ol, oi, axis=1)) == 0
+        assert_close(o1.read(np.float32, (1, s.n_embd)), want, rel_l2=5e-5)
+
+
 @pytest.mark.parametrize("n_embd,n_ff,n_expert,n_used", [
     (1024, 256, 32, 4),       # one Q6_K superblock per down row
     (1024, 512, 32, 8),
