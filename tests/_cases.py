@@ -13,14 +13,17 @@ TOL_REL_L2 = 1e-3
 
 
 class Case:
-    def __init__(self, spec: W.LayerSpec, seed: int = 1234, layer: int = 0, router: np.ndarray | None = None):
-        """router (optional): F32 router rows [E][K] in place of the generated ones."""
+    def __init__(self, spec: W.LayerSpec, seed: int = 1234, layer: int = 0, router: np.ndarray | None = None,
+                 host: W.HostLayer | None = None):
+        """router (optional): F32 router rows [E][K] in place of the generated ones.
+        host (optional): an already generated layer, whose device copy the
+        caller holds (self.dev is then None)."""
         self.spec = spec
-        self.host = W.make_layer(spec, seed, layer)
+        self.host = host if host is not None else W.make_layer(spec, seed, layer)
         if router is not None:
             assert spec.router_type == ds3.TYPE_F32
             self.host.router = np.ascontiguousarray(router, np.float32).reshape(-1).view(np.uint8)
-        self.dev = self.host.to_device()
+        self.dev = self.host.to_device() if host is None else None
         E, K, F = spec.n_expert, spec.n_embd, spec.n_ff
         self.wr = O.dequantize(spec.router_type, self.host.router, E * K).reshape(E, K)
         self.wg = O.dequantize(spec.gate_type, self.host.gate, E * F * K)
