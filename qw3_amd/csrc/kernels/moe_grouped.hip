@@ -257,16 +257,23 @@ template <bool AL> struct GgStage<T_Q8_0, AL> {
 };
 
 // Activation fragments of K-slots q0 and q0+1 for MB m blocks: lane (g, m)
-// reads row 16mb + m at its slot's chunk; all reads issued before one wait,
-// which names every result so nothing reads them early.
+// reads row 16mb + m at its slot's chunk.  gg_afrag_issue issues the reads;
+// gg_afrag_wait waits for all of them, naming every result so nothing reads
+// them early.  In between, the weight fragments are decoded, which hides the
+// LDS latency.
 template <int MB>
-__device__ __forceinline__ void gg_afrag(uint32_t a0, uint32_t a1, half8 (&af)[2][MB])
+__device__ __forceinline__ void gg_afrag_issue(uint32_t a0, uint32_t a1, half8 (&af)[2][MB])
 {
 #pragma unroll
     for (int mb = 0; mb < MB; mb++) {
         asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(af[0][mb]) : "v"(a0), "i"(16 * GG_SLICE * mb));
         asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(af[1][mb]) : "v"(a1), "i"(16 * GG_SLICE * mb));
     }
+}
+
+template <int MB>
+__device__ __forceinline__ void gg_afrag_wait(half8 (&af)[2][MB])
+{
     if constexpr (MB == 1)
         asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(af[0][0]), "+v"(af[1][0]));
     else if constexpr (MB == 2)
@@ -291,6 +298,8 @@ __device__ __forceinline__ void gg_step(const RawUnits<TYPE> (&raw)[NB], uint32_
     for (int hv = 0; hv < 2; hv++) {
 #pragma unroll
         for (int pp = 0; pp < 2; pp++) {
+            half8 af[2][MB];
+            gg_afrag_issue<MB>(sb + lofs[4 * hv + 2 * pp], sb + lofs[4 * hv + 2 * pp + 1], af);
             // only the two fragments this half step feeds stay live (the
             // compiler drops the other two and shares the scale set-up)
             half8 bq[NB][2];
@@ -301,8 +310,7 @@ __device__ __forceinline__ void gg_step(const RawUnits<TYPE> (&raw)[NB], uint32_
                 bq[nb][0] = fr[2 * pp];
                 bq[nb][1] = fr[2 * pp + 1];
             }
-            half8 af[2][MB];
-            gg_afrag<MB>(sb + lofs[4 * hv + 2 * pp], sb + lofs[4 * hv + 2 * pp + 1], af);
+            gg_afrag_wait<MB>(af);
 #pragma unroll
             for (int p = 0; p < 2; p++)
 #pragma unroll
