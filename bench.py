@@ -60,10 +60,10 @@ def parse():
     p.add_argument("--stack-layers", type=int, default=48, help="config 4: resident layers per decode step")
     p.add_argument("--stack-steps", type=int, default=50)
     p.add_argument("--no-graph", action="store_true",
-                   help="config 4: enqueue every layer eagerly instead of replaying the token's layers as one HIP graph")
+                   help="configs 4 and the T=1 leg: enqueue every call eagerly instead of replaying captured HIP graphs")
     p.add_argument("--stack-block", action="store_true",
                    help="config 4: run each layer as the engine's FFN block (RMSNorm + MoE + residual)")
-    p.add_argument("--t1-steps", type=int, default=200)
+    p.add_argument("--t1-steps", type=int, default=208)
     p.add_argument("--no-t1", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--skip", type=str, default="", help="default run: comma-separated legs to leave out (c3,c4,c5)")
@@ -87,12 +87,15 @@ def kernel_bytes(name, spec, T, counts, n_used):
     gu = F * (ds3.row_bytes(spec.gate_type, K) + ds3.row_bytes(spec.up_type, K))
     dn = K * ds3.row_bytes(spec.down_type, F)
     S = T * n_used
+    # certified routing (T <= 16): the gate/up launch also streams the router
+    # rows of every selected expert for the exact logits of the weights
+    exact = S * K * 4 if T <= 16 else 0
     return {
         "moe_grouped_gate_up": distinct * gu + T * K * 2 + S * F * 2,
         "moe_grouped_down": distinct * dn + S * F * 2 + S * K * 4,
-        "moe_decode_gate_up": distinct * gu + T * K * 4 + S * F * 4,
+        "moe_decode_gate_up": distinct * gu + T * K * 4 + S * F * 4 + exact,
         # with the certified selection in its prologue: also reads S and B
-        "moe_decode_gate_up_sel": distinct * gu + T * K * 4 + S * F * 4 + T * E * (8 + 4),
+        "moe_decode_gate_up_sel": distinct * gu + T * K * 4 + S * F * 4 + T * E * (8 + 4) + exact,
         "moe_decode_down": distinct * dn + S * F * 4 + T * K * 4,
         "router_logits": W.router_bytes(spec) + T * K * 4 + T * E * 4,
         # certified router: the sums read the router and x, write S, B and the logits;
@@ -107,12 +110,37 @@ def load_traffic(args):
     return json.loads(tpath.read_text()) if tpath.exists() else None
 
 
-def time_steps(step, steps, warmup, spec, T, n_used, first, per_kernel=True):
+def held(step):
+    """step(i) preceded by a hold of the stream long enough for the host to
+    enqueue the step before the GPU reaches it, for the passes that bracket
+    kernels with events: where the host enqueues more slowly than the GPU runs
+    (T = 1), an event pair around a kernel would otherwise also span the
+    host's launch of that kernel.  The hold is sized from the host's enqueue
+    time of one step, measured with the stream held."""
+    from qw3_amd._native import hip
+    hip().ds3_hip_synchronize()
+    hip().ds3_hip_begin_batch()
+    hip().ds3_hip_hold_stream(20000.0)
+    t0 = time.perf_counter()
+    step(0)
+    host_us = (time.perf_counter() - t0) * 1e6
+    hip().ds3_hip_end_batch()
+    hold_us = min(20000.0, 2.0 * host_us + 50.0)
+
+    def run(i):
+        hip().ds3_hip_hold_stream(hold_us)
+        step(i)
+    return run
+
+
+def time_steps(step, steps, warmup, spec, T, n_used, first, per_kernel=True, graph_of=0):
     """`first()` runs one step and returns the routed indices [T][n_used];
     then warmup steps with every kernel timed (breakdown, dominant kernel),
     the timed steps with no per-kernel events, and the same steps again with
-    only the dominant kernel bracketed by events.  Returns (wall_ms, gpu_ms,
-    stats, breakdown, counts)."""
+    only the dominant kernel bracketed by events.  With graph_of = G > 0 the
+    timed steps are replays of one HIP graph of steps 0 .. G-1 (steps a
+    multiple of G), as a decode loop replays its captured calls.  Returns
+    (wall_ms, gpu_ms, stats, breakdown, counts)."""
     from qw3_amd import ds3
     from qw3_amd._native import hip
     E = spec.n_expert
@@ -120,30 +148,45 @@ def time_steps(step, steps, warmup, spec, T, n_used, first, per_kernel=True):
     hip().ds3_hip_synchronize()
     counts = np.bincount(idx.reshape(-1), minlength=E)
     brk, dominant = {}, None
+    hstep = held(step) if per_kernel else step
     if per_kernel:
         hip().ds3_hip_kernel_timing_only(None)
         hip().ds3_hip_kernel_timing_reset()
         hip().ds3_hip_kernel_timing(1)
     hip().ds3_hip_begin_batch()
     for i in range(1, warmup + 1):
-        step(i)
+        hstep(i)
     hip().ds3_hip_end_batch()
     if per_kernel:
         hip().ds3_hip_kernel_timing(0)
         brk = ds3.kernel_stats()
         dominant = max((k for k in brk if kernel_bytes(k, spec, T, counts, n_used) is not None),
                        key=lambda k: brk[k][1])
+    graph = None
+    if graph_of:
+        assert steps % graph_of == 0
+        graph = ds3.Graph()
+        with graph:
+            for i in range(graph_of):
+                step(i)
+        graph.launch()                          # one untimed replay
     # timed region: synchronise, K steps enqueued back to back, synchronise;
     # no per-kernel events in it (at T = 1 an event pair costs a third of a step)
     hip().ds3_hip_synchronize()
     hip().ds3_hip_begin_batch()
     t0 = time.perf_counter()
     hip().ds3_hip_timer_start()
-    for i in range(steps):
-        step(i)
+    if graph is not None:
+        for _ in range(steps // graph_of):
+            graph.launch()
+    else:
+        for i in range(steps):
+            step(i)
     gpu_ms = hip().ds3_hip_timer_stop_ms()
     hip().ds3_hip_end_batch()
     wall_ms = (time.perf_counter() - t0) * 1e3
+    if graph is not None:
+        graph.close()
     stats = {}
     if per_kernel:
         # the same steps again with only the dominant kernel bracketed by
@@ -153,7 +196,7 @@ def time_steps(step, steps, warmup, spec, T, n_used, first, per_kernel=True):
         hip().ds3_hip_kernel_timing(1)
         hip().ds3_hip_begin_batch()
         for i in range(steps):
-            step(i)
+            hstep(i)
         hip().ds3_hip_end_batch()
         hip().ds3_hip_kernel_timing(0)
         hip().ds3_hip_kernel_timing_only(None)
@@ -313,13 +356,15 @@ def make_layers(spec, n, what):
     return hosts[0], layers
 
 
-def leg_layer(args, config, T, steps, warmup, spec, layers, xs, traffic, n_used=8, what=""):
+def leg_layer(args, config, T, steps, warmup, spec, layers, xs, traffic, n_used=8, what="", graph_of=0):
     """One layer call per step on T tokens: figures, dominant-kernel roofline."""
     from qw3_amd import workload as W
     step, first = layer_steps(T, layers, xs, spec, n_used)
-    wall_ms, gpu_ms, stats, brk, counts = time_steps(step, steps, warmup, spec, T, n_used, first)
+    wall_ms, gpu_ms, stats, brk, counts = time_steps(step, steps, warmup, spec, T, n_used, first,
+                                                     graph_of=graph_of)
     ms = wall_ms / steps
-    log(f"[bench] {what} T={T}: {ms * 1e3:.1f} us/step wall, {gpu_ms / steps * 1e3:.1f} us/step events")
+    log(f"[bench] {what} T={T}: {ms * 1e3:.1f} us/step wall, {gpu_ms / steps * 1e3:.1f} us/step events"
+        + (f", steps replayed as HIP graphs of {graph_of}" if graph_of else ""))
     log_breakdown(brk, stats)
     distinct = int((counts > 0).sum())
     b = W.algorithmic_bytes(spec, T, distinct)
@@ -468,12 +513,13 @@ def leg_stack(args, traffic, n_used=8):
     steps = args.stack_steps
     idx0 = first()
     counts = np.bincount(idx0, minlength=E)
+    htoken = held(token)
     hip().ds3_hip_kernel_timing_only(None)
     hip().ds3_hip_kernel_timing_reset()
     hip().ds3_hip_kernel_timing(1)
     hip().ds3_hip_begin_batch()
     for i in range(1, 3):
-        token(i)
+        htoken(i)
     hip().ds3_hip_end_batch()
     hip().ds3_hip_kernel_timing(0)
     brk = ds3.kernel_stats()
@@ -494,7 +540,7 @@ def leg_stack(args, traffic, n_used=8):
     hip().ds3_hip_kernel_timing(1)
     hip().ds3_hip_begin_batch()
     for i in range(steps):
-        token(i)
+        htoken(i)
     hip().ds3_hip_end_batch()
     hip().ds3_hip_kernel_timing(0)
     hip().ds3_hip_kernel_timing_only(None)
@@ -647,7 +693,13 @@ def main():
         layers1 = [W.make_layer(spec1, seed=1234, layer=l).to_device() for l in range(args.layers)]
         x1h = [W.make_inputs(1, 1, seed=98, step=s) for s in range(16)]
         x1 = [ds3.Buffer.from_array(x) for x in x1h]
-        t1 = leg_layer(args, 1, 1, args.t1_steps, args.warmup, spec1, layers1, x1, traffic, what="t1")
+        # decode: the timed steps replay a HIP graph of 16 steps (every layer
+        # and input pair once), as a decode loop replays its captured calls
+        # (--no-graph: each step enqueued from Python)
+        g = 0 if args.no_graph else 16
+        t1_steps = args.t1_steps if not g else max(g, args.t1_steps // g * g)
+        t1 = leg_layer(args, 1, 1, t1_steps, args.warmup, spec1, layers1, x1, traffic, what="t1", graph_of=g)
+        t1["graph"] = bool(g)
         for k in ("mfma_util", "expert_histogram", "tokens"):
             t1.pop(k, None)
         if not args.no_cpu:

@@ -316,6 +316,14 @@ void ds3_hip_kernel_timing_only(const char *name);
 void ds3_hip_kernel_timing_reset(void);
 int  ds3_hip_kernel_stats(int i, char *name, size_t name_len, int64_t *count, double *total_ms);
 
+/* Occupies the library stream for `us` microseconds (0 .. 1e6) with one
+ * wave that touches no memory.  Enqueued ahead of kernels timed with
+ * ds3_hip_kernel_timing when the host enqueues more slowly than the GPU runs
+ * them (few tokens): the held stream lets the host queue the work first, so
+ * that each event pair spans its kernel and not the host's enqueue.
+ * Refused during graph capture. */
+int ds3_hip_hold_stream(double us);
+
 /* Event pair on the library stream around a caller-defined region. */
 int    ds3_hip_timer_start(void);
 double ds3_hip_timer_stop_ms(void);

@@ -79,6 +79,7 @@ SIGNATURES: dict[str, tuple] = {
     "ds3_hip_kernel_timing_reset": (None, []),
     "ds3_hip_kernel_timing_only": (None, [C.c_char_p]),
     "ds3_hip_kernel_stats": (C.c_int, [C.c_int, C.c_char_p, SZ, C.POINTER(I64), C.POINTER(D)]),
+    "ds3_hip_hold_stream": (C.c_int, [D]),
     "ds3_hip_timer_start": (C.c_int, []),
     "ds3_hip_timer_stop_ms": (D, []),
     "ds3_hip_device_info": (C.c_int, [C.c_char_p, SZ, C.POINTER(C.c_int), C.POINTER(U64)]),

@@ -191,7 +191,8 @@ struct Bump {
     }
 };
 
-// RAII event pair around one kernel launch while kernel timing is on.
+// RAII event pair around one launcher call while kernel timing is on
+// (timing-only events: no system-scope fence when recorded).
 struct KScope {
     int e0 = -1;
     const char *name;
@@ -1566,8 +1567,11 @@ extern "C" void ds3_hip_kernel_timing(int enable)
         return;
     }
     if (enable && g.pool.empty()) {
+        // timing-only events: no system-scope fence (and its L2 writeback)
+        // when recorded, which would otherwise add several microseconds to
+        // every bracketed kernel
         g.pool.resize(16384);
-        for (auto &e : g.pool) (void)hipEventCreate(&e);
+        for (auto &e : g.pool) (void)hipEventCreateWithFlags(&e, hipEventDisableSystemFence);
     }
     g.ktiming = enable != 0;
 }
@@ -1636,6 +1640,12 @@ extern "C" double ds3_hip_timer_stop_ms(void)
     float ms = 0.f;
     (void)hipEventElapsedTime(&ms, g.t0, g.t1);
     return ms;
+}
+
+extern "C" int ds3_hip_hold_stream(double us)
+{
+    if (refuse_in_capture("hold_stream") || !ensure_init()) return -1;
+    return report(ds3k::launch_hold(us, g.stream), "hold_stream");
 }
 
 extern "C" int ds3_hip_device_info(char *arch, size_t arch_len, int *n_cu, uint64_t *hbm_bytes)

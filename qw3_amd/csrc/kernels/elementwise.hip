@@ -31,6 +31,16 @@ __global__ void k_fill_zero4(float *p, int64_t n)
         for (int64_t j = 4 * n4; j < n; j++) p[j] = 0.0f;
 }
 
+// Keeps one wave busy for `ticks` of the 100 MHz real-time counter, then
+// exits; touches no memory.  Launched ahead of work whose kernels are timed
+// with events, so that the host can enqueue that work before the stream
+// reaches it.
+__global__ void __launch_bounds__(64) k_hold(uint64_t ticks)
+{
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__builtin_amdgcn_s_memrealtime() - t0 < ticks) __builtin_amdgcn_s_sleep(64);
+}
+
 __global__ void k_copy(const float *a, float *b, int64_t n)
 {
     const int64_t i = (int64_t)blockIdx.x * EW_TPB + threadIdx.x;
@@ -171,6 +181,13 @@ hipError_t launch_fill_zero(float *p, int64_t n, hipStream_t s)
                            n);
     }
     else hipLaunchKernelGGL(k_fill_zero, grid1d(n), dim3(EW_TPB), 0, s, p, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_hold(double us, hipStream_t s)
+{
+    if (!(us >= 0.0 && us <= 1e6)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_hold, dim3(1), dim3(64), 0, s, (uint64_t)(us * 100.0));
     return hipGetLastError();
 }
 

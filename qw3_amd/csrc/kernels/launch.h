@@ -189,6 +189,8 @@ hipError_t launch_rms_norm(const float *x, const float *w, float *out, int n, in
 // Elementwise helpers (reference metal/elementwise.metal, metal/moe.metal:95-127).
 hipError_t launch_fill_zero(float *p, int64_t n, hipStream_t s);
 hipError_t launch_copy(const float *a, float *b, int64_t n, hipStream_t s);
+// One wave that waits `us` microseconds (at most one second) on the GPU.
+hipError_t launch_hold(double us, hipStream_t s);
 hipError_t launch_add(const float *a, const float *b, float *c, int64_t n, hipStream_t s);
 // Row ids outside [0, n_rows) are skipped.
 hipError_t launch_gather_rows(const float *src, const int32_t *ids, float *dst, int n_cols, int count,
