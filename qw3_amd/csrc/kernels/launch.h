@@ -168,9 +168,10 @@ hipError_t launch_grouped_gate_up(const _Float16 *x16, int K, const ExpertWeight
 hipError_t launch_grouped_down(const _Float16 *h16, int F, const ExpertWeights &ew, int N,
                                const BucketOut &b, float *y, hipStream_t s);
 bool grouped_type_ok(int type, int K);
-// Layer shapes the grouped kernels take: n_embd a multiple of 512 (gate_up's
-// activation chunks), n_ff a multiple of 128 and at most 1024 (down's token
-// tile stays in LDS).
+// Layer shapes the grouped kernels take: n_embd a multiple of 256 x gate_up's
+// weight ring depth (512 as built: whole activation chunks and ring turns per
+// n tile), n_ff a multiple of 128 and at most 1024 (down's token tile stays
+// in LDS).
 bool grouped_shape_ok(int n_embd, int n_ff);
 // n-runs per token tile of the grouped kernels for a layer shape (BucketOut
 // rpi_gu / rpi_dn).

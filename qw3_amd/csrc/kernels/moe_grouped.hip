@@ -409,10 +409,10 @@ __device__ __forceinline__ void gg_run_chunked(const uint8_t *const (&rows)[2], 
     constexpr int NB = 2, BLK = GgBlk<TYPE>::BLK;
     using St = GgStage<TYPE, AL>;
     constexpr int NW = NB * St::NLOAD;
-    static_assert(NA + (D - 1) * NW <= 63 && D * NW <= 63, "vmcnt field holds 0..63");
-    // one loop iteration is one chunk and one turn of the ring, so both stay
-    // in step across n tiles (K a multiple of 512: whole chunks per n tile)
-    static_assert(D == GG_CHUNK_STEPS, "the chunked K loop turns the weight ring once per chunk");
+    static_assert(NA + (D - 1) * NW <= 63, "vmcnt field holds 0..63");
+    // one loop iteration is D steps: whole chunks and one turn of the ring,
+    // so both stay in step across n tiles (K a multiple of 256 * D)
+    static_assert(D % GG_CHUNK_STEPS == 0, "the chunked K loop turns the weight ring once per D / 2 chunks");
     constexpr int UNR = D;
     const int U = nnt * S;
     floatx4 acc[MB][NB];
@@ -767,7 +767,7 @@ bool grouped_type_ok(int type, int K)
 
 bool grouped_shape_ok(int n_embd, int n_ff)
 {
-    return n_embd % (256 * GG_CHUNK_STEPS) == 0 && n_ff % GG_TILE_N == 0 && n_embd % GG_TILE_N == 0 &&
+    return n_embd % (256 * DS3_GU_DEPTH) == 0 && n_ff % GG_TILE_N == 0 && n_embd % GG_TILE_N == 0 &&
            n_ff <= GG_DN_MAXK;
 }
 

@@ -630,10 +630,16 @@ __device__ __forceinline__ float chain_block(float acc, const float4 &wq, const 
 // consecutive elements of each of 8 experts); wave 0 (the consumer) reads
 // each expert's 32 products in order with 8 LDS reads and adds them.  One
 // workgroup barrier per chunk of XC_CH blocks hands a product buffer over.
-constexpr int XC_CH = 4;        // blocks per chunk
+#ifndef DS3_XC_CH
+#define DS3_XC_CH 4
+#endif
+#ifndef DS3_XC_RP
+#define DS3_XC_RP 7
+#endif
+constexpr int XC_CH = DS3_XC_CH;        // blocks per chunk
 constexpr int XC_PS = 36;       // floats per expert in a block's products: 32 + 4 (conflict-free reads)
 constexpr int XC_NP = 3;        // producer waves
-constexpr int XC_RP = 7;        // DMA ring slots (1 KiB blocks) per producer wave: ~1.4 us of lookahead
+constexpr int XC_RP = DS3_XC_RP;        // DMA ring slots (1 KiB blocks) per producer wave: ~1.4 us of lookahead
 constexpr int XC_THREADS = (XC_NP + 1) * WAVE;
 
 // LDS of the exact stage: the token's row (K floats), two product buffers,
