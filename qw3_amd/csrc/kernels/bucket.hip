@@ -132,19 +132,35 @@ k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int 
     }
     __syncthreads();
     if (o.runs_gu != nullptr) {
-        // run lists: (tile, n-run) for every tile, gate_up's and down's
-        int rg = e < E ? ntile * o.rpi_gu : 0, rd = e < E ? ntile * o.rpi_dn : 0;
-        int tg = 0, td = 0;
-        block_scan2(rg, rd, tg, td, E, wsum);
+        // run lists: (tile, n-run) for every tile, gate_up's and down's,
+        // heaviest first: tiles of 4 m blocks (16-token blocks), then 3, 2, 1,
+        // each class in tile order.  A run's cost grows with its m blocks,
+        // and the grouped kernels deal the list out round by round, so the
+        // rounds then hold runs of like cost.  Only an expert's last tile can
+        // have fewer than 4 m blocks.
+        const int full = cnt / o.tile_m, rest = cnt - full * o.tile_m;
+        const int mb_last = rest > 0 ? (4 * rest + o.tile_m - 1) / o.tile_m : 0;   // quarters of a tile: 1 .. 4
+        int a4 = e < E ? full + (mb_last == 4 ? 1 : 0) : 0, a3 = e < E && mb_last == 3 ? 1 : 0;
+        int a2 = e < E && mb_last == 2 ? 1 : 0, a1 = e < E && mb_last == 1 ? 1 : 0;
+        int n4 = 0, n3 = 0, n2 = 0, n1 = 0;
+        block_scan2(a4, a3, n4, n3, E, wsum);
+        __syncthreads();                                  // wsum is read before the next scan writes it
+        block_scan2(a2, a1, n2, n1, E, wsum);
         if (e < E) {
+            // position of this expert's first tile of each class among all tiles
+            const int cls_pos[5] = { 0, n4 + n3 + n2 + a1, n4 + n3 + a2, n4 + a3, a4 };
             for (int m = 0; m < ntile && tb + m < o.max_tiles; m++) {
-                for (int j = 0; j < o.rpi_gu; j++) o.runs_gu[rg++] = ((tb + m) << 12) | j;
-                for (int j = 0; j < o.rpi_dn; j++) o.runs_dn[rd++] = ((tb + m) << 12) | j;
+                const int cls = m < full ? 4 : mb_last;
+                const int q = cls_pos[cls] + (cls == 4 ? m : 0);
+                if (q >= o.max_tiles) continue;
+                for (int j = 0; j < o.rpi_gu; j++) o.runs_gu[q * o.rpi_gu + j] = ((tb + m) << 12) | j;
+                for (int j = 0; j < o.rpi_dn; j++) o.runs_dn[q * o.rpi_dn + j] = ((tb + m) << 12) | j;
             }
         }
         if (threadIdx.x == 0) {
-            o.n_runs[0] = tg;
-            o.n_runs[1] = td;
+            const int nt = n4 + n3 + n2 + n1 < o.max_tiles ? n4 + n3 + n2 + n1 : o.max_tiles;
+            o.n_runs[0] = nt * o.rpi_gu;
+            o.n_runs[1] = nt * o.rpi_dn;
         }
     }
     __syncthreads();

@@ -536,15 +536,18 @@ __device__ __forceinline__ bool gg_item(const BucketOut &b, int item, GgItem &it
     return true;
 }
 
-// Persistent schedule over the bucketing kernel's run list: round k of the
-// grid (gridDim.x a multiple of 8; workgroup w sits on XCD w % 8) takes list
-// entries k*G .. k*G+G-1, consecutive entries on the same XCD, so the two
-// halves of a token tile (adjacent in the list) stream the same weights
-// through one L2 at the same time.
+// Persistent schedule over the bucketing kernel's run list (heaviest runs
+// first): round k of the grid (gridDim.x a multiple of 8; workgroup w sits on
+// XCD w % 8) takes list entries k*G .. k*G+G-1, consecutive entries on the
+// same XCD, so token tiles of one expert (adjacent in the list) stream the
+// same weights through one L2 at the same time.  Odd rounds go through their
+// entries in reverse, so the workgroup that took the heaviest run of one
+// round takes the lightest of the next.
 __device__ __forceinline__ int gg_list_index(int k)
 {
     const int G = (int)gridDim.x, w = (int)blockIdx.x;
-    return k * G + (G / N_XCD) * (w % N_XCD) + w / N_XCD;
+    const int s = (G / N_XCD) * (w % N_XCD) + w / N_XCD;
+    return k * G + ((k & 1) ? G - 1 - s : s);
 }
 
 // gate_up epilogue: h = silu(gate) * up as fp16, staged through a per-wave
