@@ -14,6 +14,8 @@
 // renorm): probabilities exp(l - max) / sum, k rounds of selection by (prob
 // desc, index asc), then weights divided by their sum.  One wavefront per
 // token.
+#include <utility>
+
 #include "route_select.h"
 
 namespace ds3k {
@@ -69,8 +71,9 @@ k_router_rows_f32(const uint8_t *__restrict__ rw, uint64_t rstride, int E, int K
 // lane.  The 16 W rows and 16 x rows stream through an LDS ring of D stages
 // of 256-wide chunks by global_load_lds DMAs, so D-1 chunks are in flight
 // while one is summed.  Rows are padded to 260 floats: the 16 lanes of each
-// ds_read_b128 pass read 16 different W rows (16 different bank groups) and
-// one x row (a broadcast).  With x16 != nullptr the workgroups of expert
+// ds_read_b128 pass read 16 different W rows (16 different bank groups).  x
+// is read one element per lane per 16-element block and reaches the other
+// lanes of its 16-lane row by DPP broadcast (rs_sum).  With x16 != nullptr the workgroups of expert
 // group 0 also write the fp16 copy of x that the grouped products read.
 // DW: DMA width in bytes, 16 (rows 16-byte aligned, K % 4 == 0) or 4.
 // ---------------------------------------------------------------------------
@@ -81,36 +84,59 @@ constexpr int RS_CH = 256;                  // floats per row chunk
 constexpr int RS_ROWB = (RS_CH + 4) * 4;    // bytes per padded LDS row
 constexpr int RS_STAGE = 32 * RS_ROWB;      // 16 W rows + 16 x rows
 
-// LDS reads of 16-element block blk (a constant once unrolled) of a lane's W
-// row (LDS byte address wa) and of its token's x row (xa), 4 x 16 bytes each.
-__device__ __forceinline__ void rs_read(int blk, uint32_t wa, uint32_t xa, u32x4 (&w)[4], u32x4 (&x)[4])
+// LDS reads of 16-element block blk (a constant once unrolled): 4 x 16
+// bytes of the lane's W row (LDS byte address wa), and one element of its
+// token's x row: lane l of each 16-lane row reads element l of the block
+// (xa already includes 4 * (lane % 16)).  The 16 lanes of a row sum the
+// same token, so the mul of element i takes x from lane i of the row by a
+// DPP row broadcast instead of every lane reading all 16 elements: a
+// quarter of the LDS bytes of 16-byte x reads per lane.
+__device__ __forceinline__ void rs_read(int blk, uint32_t wa, uint32_t xa, u32x4 (&w)[4], uint32_t &x)
 {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < 4; i++)
         asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(w[i]) : "v"(wa), "i"(64 * blk + 16 * i) : "memory");
-        asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(x[i]) : "v"(xa), "i"(64 * blk + 16 * i) : "memory");
-    }
+    asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(x) : "v"(xa), "i"(64 * blk) : "memory");
 }
 
-// Wait until at most N LDS reads are outstanding: with the 8 reads of the
-// next block issued after these, N = 8 releases exactly this block.
+// Wait until at most N LDS reads are outstanding: with the 5 reads of the
+// next block issued after these, N = 5 releases exactly this block.
 template <int N>
-__device__ __forceinline__ void rs_wait(u32x4 (&w)[4], u32x4 (&x)[4])
+__device__ __forceinline__ void rs_wait(u32x4 (&w)[4], uint32_t &x)
 {
-    asm volatile("s_waitcnt lgkmcnt(%8)"
-                 : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3])
-                 : "i"(N));
+    asm volatile("s_waitcnt lgkmcnt(%5)" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]), "+v"(x) : "i"(N));
+}
+
+// x[i] of the lane's token: element i of the block from lane i of the
+// lane's 16-lane row (DPP row_newbcast, folded into the multiply).
+template <int I>
+__device__ __forceinline__ float rs_bcast(uint32_t x)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp((int)x, 0x150 + I, 0xf, 0xf, true));
 }
 
 // acc += x[i] * w[i] for the block's 16 elements in order, the product and
-// the sum rounded separately.
-__device__ __forceinline__ void rs_sum(float &acc, const u32x4 (&w)[4], const u32x4 (&x)[4])
+// the sum rounded separately (the folds run left to right).  One wave per
+// SIMD sums its chains, so the time is the latency of the dependent adds:
+// the 16 products are all issued first (the empty asm takes them as
+// operands), and the adds then wait only on each other, not each on the
+// multiply issued just before it.
+template <int... I>
+__device__ __forceinline__ void rs_sum_seq(float &acc, const u32x4 (&w)[4], uint32_t x,
+                                           std::integer_sequence<int, I...>)
 {
 #pragma clang fp contract(off)
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc = acc + __uint_as_float(x[i][j]) * __uint_as_float(w[i][j]);
+    float p[16];
+    ((p[I] = rs_bcast<I>(x) * __uint_as_float(w[I / 4][I % 4])), ...);
+    asm volatile("" : "+v"(p[0]), "+v"(p[1]), "+v"(p[2]), "+v"(p[3]), "+v"(p[4]), "+v"(p[5]), "+v"(p[6]),
+                 "+v"(p[7]), "+v"(p[8]), "+v"(p[9]), "+v"(p[10]), "+v"(p[11]), "+v"(p[12]), "+v"(p[13]),
+                 "+v"(p[14]), "+v"(p[15]));
+    ((acc = acc + p[I]), ...);
+}
+
+__device__ __forceinline__ void rs_sum(float &acc, const u32x4 (&w)[4], uint32_t x)
+{
+    rs_sum_seq(acc, w, x, std::make_integer_sequence<int, 16>{});
 }
 
 // This wave's vector-memory loads (the ring's DMAs): wait until at most n
@@ -209,6 +235,7 @@ k_router_seq(const float *__restrict__ x, int T, int K, int E, const float *__re
     const int my_t = t0 + 4 * wave + (lane >> 4), my_e = e0 + (lane & 15);
     const uint32_t w_off = (uint32_t)((lane & 15) * RS_ROWB);
     const uint32_t x_off = (uint32_t)((16 + 4 * wave + (lane >> 4)) * RS_ROWB);
+    const uint32_t xl_off = x_off + 4u * (uint32_t)(lane & 15);      // this lane's element of each x block
     const bool put16 = x16 != nullptr && blockIdx.y == 0;
 
 #pragma unroll
@@ -220,21 +247,22 @@ k_router_seq(const float *__restrict__ x, int T, int K, int E, const float *__re
         rs_barrier();                                 // everyone's have; stage (c-1) % D is free
         if (c + D - 1 < nch) issue(c + D - 1);
         const uint32_t st = lds0 + (uint32_t)((c % D) * RS_STAGE);
-        const uint32_t wa = st + w_off, xa = st + x_off;
+        const uint32_t wa = st + w_off, xa = st + x_off, xla = st + xl_off;
         const int kn = min(RS_CH, K - c * RS_CH);
         if (kn == RS_CH) {
             // 16-element blocks, two register sets: the reads of block i+1
             // are issued before block i is summed
-            u32x4 w0[4], x0[4], w1[4], x1[4];
-            rs_read(0, wa, xa, w0, x0);
+            u32x4 w0[4], w1[4];
+            uint32_t x0, x1;
+            rs_read(0, wa, xla, w0, x0);
 #pragma unroll
             for (int blk = 0; blk < RS_CH / 16; blk += 2) {
-                rs_read(blk + 1, wa, xa, w1, x1);
-                rs_wait<8>(w0, x0);
+                rs_read(blk + 1, wa, xla, w1, x1);
+                rs_wait<5>(w0, x0);
                 rs_sum(acc, w0, x0);
                 if (blk + 2 < RS_CH / 16) {
-                    rs_read(blk + 2, wa, xa, w0, x0);
-                    rs_wait<8>(w1, x1);
+                    rs_read(blk + 2, wa, xla, w0, x0);
+                    rs_wait<5>(w1, x1);
                 } else {
                     rs_wait<0>(w1, x1);
                 }
