@@ -521,10 +521,15 @@ template <> struct RawUnits<T_Q6_K> {
 #pragma unroll
             for (int ww = 0; ww < 2; ww++) {
                 const uint32_t ql = (t & 1) ? v[1][ww] : v[0][ww];
+                const uint32_t qh = v[2][ww];
+                // code = nibble | (2 high bits << 4) per byte, as one bitfield insert: the
+                // nibble (bits 0-3 of ql for t < 2, bits 4-7 for t >= 2) under the mask,
+                // qh shifted so that field t (bits 2t, 2t+1) lands on bits 4-5; bits 6-7
+                // of each byte keep whatever falls there, and fma4's 6-bit mask drops them.
+                // Bytes 0/2 and 1/3 feed the two fp16 lanes.
                 const uint32_t nib = (t < 2) ? ql : (ql >> 4);
-                const uint32_t hb = v[2][ww] >> (2 * t);
-                // code = nibble | (2 high bits << 4) per byte; bytes 0/2 and 1/3 feed the two fp16 lanes
-                const uint32_t code = (nib & 0x0f0f0f0fu) | ((hb & 0x03030303u) << 4);
+                const uint32_t hs = t == 0 ? qh << 4 : t == 1 ? qh << 2 : t == 2 ? qh : qh >> 2;
+                const uint32_t code = (nib & 0x0f0f0f0fu) | (hs & 0xf0f0f0f0u);
                 fma4(code, code >> 8, 0x003f003fu, mg, ds, cs, w + 4 * ww);
             }
 #pragma unroll
