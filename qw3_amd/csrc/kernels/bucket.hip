@@ -108,15 +108,32 @@ k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int 
         if (threadIdx.x + BUCKET_TPB * i < S) mark(threadIdx.x + BUCKET_TPB * i, ex_c[i]);
     for (int s = threadIdx.x + BUCKET_TPB * BUCKET_CACHE; s < S; s += BUCKET_TPB) mark(s, idx[s]);
     __syncthreads();
-    // thread e: its expert's per-chunk prefix, count and work items
+    // Per-chunk prefixes of each expert's bits: G = BUCKET_TPB / E threads per
+    // expert, thread (g, e) = g * E + e owns a run of consecutive chunks; run
+    // totals meet in off_s (free until the offsets), then each thread writes
+    // its run's prefixes.  Thread e then holds its expert's count.
     const int e = threadIdx.x;                            // E <= BUCKET_TPB
-    int cnt = 0;
-    if (e < E) {
-        for (int c = 0; c < chunks; c++) {
-            pre[c * E + e] = (uint16_t)cnt;
-            cnt += __popc(mask[c * E + e]);
+    {
+        const int G = BUCKET_TPB / E, gi = threadIdx.x / E, ei = threadIdx.x - gi * E;
+        const int L = (chunks + G - 1) / G, c0 = gi * L, c1 = min(chunks, c0 + L);
+        int part = 0;
+        if (gi < G)
+            for (int c = c0; c < c1; c++) part += __popc(mask[c * E + ei]);
+        off_s[threadIdx.x] = part;
+        __syncthreads();
+        if (gi < G) {
+            int run = 0;
+            for (int g = 0; g < gi; g++) run += off_s[g * E + ei];
+            for (int c = c0; c < c1; c++) {
+                pre[c * E + ei] = (uint16_t)run;
+                run += __popc(mask[c * E + ei]);
+            }
         }
     }
+    int cnt = 0;
+    if (e < E)
+        for (int g = 0; g < BUCKET_TPB / E; g++) cnt += off_s[g * E + e];
+    __syncthreads();                                      // off_s is read before it is rewritten
     int off = cnt, tb = (cnt + o.tile_m - 1) / o.tile_m, total = 0, total_t = 0;
     const int ntile = tb;
     block_scan2(off, tb, total, total_t, E, wsum);
@@ -124,14 +141,27 @@ k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int 
         o.counts[e] = cnt;
         o.offsets[e] = off;
         off_s[e] = off;
-        for (int m = 0; m < ntile && tb + m < o.max_tiles; m++) o.tiles[tb + m] = (e << 16) | m;
     }
     if (threadIdx.x == 0) {
         o.offsets[E] = total;
         *o.n_tiles = total_t < o.max_tiles ? total_t : o.max_tiles;
     }
-    __syncthreads();
-    if (o.runs_gu != nullptr) {
+    // Per-expert tile facts in the staging area (free until the placement):
+    // each tile's expert, each expert's first tile, and for the run lists the
+    // tile counts by cost class.
+    const int nt = total_t < o.max_tiles ? total_t : o.max_tiles;
+    uint32_t *xs = sm + bucket_stage_words(chunks, E);
+    int *tb_s = (int *)xs;                        // [E] first tile of each expert
+    uint32_t *info_s = xs + E;                    // [E] full tiles << 16 | m blocks of the last tile
+    uint32_t *cpos_s = info_s + E;                // [E] class-4 position << 16 | last tile's class position
+    uint16_t *own_s = (uint16_t *)(cpos_s + E);   // [nt] expert of each tile
+    if (e < E) {
+        tb_s[e] = tb;
+        for (int m = 0; m < ntile && tb + m < nt; m++) own_s[tb + m] = (uint16_t)e;
+    }
+    const bool runs = o.runs_gu != nullptr;
+    __syncthreads();                                      // wsum is read before the next scan writes it
+    if (runs) {
         // run lists: (tile, n-run) for every tile, gate_up's and down's,
         // heaviest first: tiles of 4 m blocks (16-token blocks), then 3, 2, 1,
         // each class in tile order.  A run's cost grows with its m blocks,
@@ -147,21 +177,31 @@ k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int 
         __syncthreads();                                  // wsum is read before the next scan writes it
         block_scan2(a2, a1, n2, n1, E, wsum);
         if (e < E) {
-            // position of this expert's first tile of each class among all tiles
-            const int cls_pos[5] = { 0, n4 + n3 + n2 + a1, n4 + n3 + a2, n4 + a3, a4 };
-            for (int m = 0; m < ntile && tb + m < o.max_tiles; m++) {
-                const int cls = m < full ? 4 : mb_last;
-                const int q = cls_pos[cls] + (cls == 4 ? m : 0);
-                if (q >= o.max_tiles) continue;
-                for (int j = 0; j < o.rpi_gu; j++) o.runs_gu[q * o.rpi_gu + j] = ((tb + m) << 12) | j;
-                for (int j = 0; j < o.rpi_dn; j++) o.runs_dn[q * o.rpi_dn + j] = ((tb + m) << 12) | j;
+            // position among all tiles of this expert's first class-4 tile and of its last tile
+            const int last = mb_last == 4 || mb_last == 0 ? 0
+                           : mb_last == 3 ? n4 + a3 : mb_last == 2 ? n4 + n3 + a2 : n4 + n3 + n2 + a1;
+            info_s[e] = ((uint32_t)full << 16) | (uint32_t)mb_last;
+            cpos_s[e] = ((uint32_t)a4 << 16) | (uint32_t)last;
+        }
+    }
+    __syncthreads();
+    // One thread per tile (work item) writes its work item and runs.
+    for (int q = threadIdx.x; q < nt; q += BUCKET_TPB) {
+        const int lo = own_s[q], m = q - tb_s[lo];
+        o.tiles[q] = (lo << 16) | m;
+        if (runs) {
+            const uint32_t inf = info_s[lo], cp = cpos_s[lo];
+            const bool c4 = m < (int)(inf >> 16) || (inf & 0xffffu) == 4u;
+            const int pos = c4 ? (int)(cp >> 16) + m : (int)(cp & 0xffffu);
+            if (pos < o.max_tiles) {
+                for (int j = 0; j < o.rpi_gu; j++) o.runs_gu[pos * o.rpi_gu + j] = (q << 12) | j;
+                for (int j = 0; j < o.rpi_dn; j++) o.runs_dn[pos * o.rpi_dn + j] = (q << 12) | j;
             }
         }
-        if (threadIdx.x == 0) {
-            const int nt = n4 + n3 + n2 + n1 < o.max_tiles ? n4 + n3 + n2 + n1 : o.max_tiles;
-            o.n_runs[0] = nt * o.rpi_gu;
-            o.n_runs[1] = nt * o.rpi_dn;
-        }
+    }
+    if (runs && threadIdx.x == 0) {
+        o.n_runs[0] = nt * o.rpi_gu;
+        o.n_runs[1] = nt * o.rpi_dn;
     }
     __syncthreads();
     auto place = [&](int s, int ex, float sc) {
@@ -200,7 +240,10 @@ hipError_t launch_bucket(const int32_t *idx, const float *scores, int T, int k, 
 {
     const int chunks = (T + 31) / 32;
     const size_t lds = (size_t)chunks * E * (sizeof(uint32_t) + sizeof(uint16_t));
-    if (T <= 0 || T > 65535 || k <= 0 || E <= 0 || E > 1024 || lds > BUCKET_MASK_BYTES)
+    if (T <= 0 || T > 65535 || k <= 0 || E <= 0 || E > 1024 || lds > BUCKET_MASK_BYTES || o.max_tiles < 0)
+        return hipErrorInvalidValue;
+    // the per-expert tile facts and the tile owner table share the staging area
+    if (bucket_stage_words(chunks, E) * 4 + (size_t)3 * E * 4 + (size_t)o.max_tiles * 2 > BUCKET_LDS_BYTES)
         return hipErrorInvalidValue;
     const size_t staged = bucket_stage_words(chunks, E) * 4 + (size_t)T * k * (sizeof(float) + sizeof(uint16_t));
     const int stage = staged <= BUCKET_LDS_BYTES ? 1 : 0;
