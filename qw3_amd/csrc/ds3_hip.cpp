@@ -791,9 +791,10 @@ bool use_cert(const float *x, int T, uint32_t n_embd, uint32_t n_expert, uint32_
 int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstride, int rtype, int T, uint32_t n_embd,
                  uint32_t n_expert, uint32_t n_used, bool norm, const RouteBufs &rb, bool *x16_done = nullptr,
                  bool allow_cert = false, DeferredSel *defer = nullptr, const NormPro *np = nullptr,
-                 ExactTail *exact = nullptr)
+                 ExactTail *exact = nullptr, uint8_t *masks = nullptr, bool *marked = nullptr)
 {
     if (exact) *exact = ExactTail{};
+    if (marked) *marked = false;
     RouteArgs ra{};
     ra.logits = rb.logits;
     ra.idx = rb.idx;
@@ -849,6 +850,12 @@ int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstrid
     if (x16_done) *x16_done = rb.x16 != nullptr;
     if (topk_done) return 0;                    // the router kernel also selected the experts
     KScope ks("router_topk");
+    if (masks != nullptr) {
+        // also the 4-token bitmaps the grouped path's placement reads
+        e = launch_route_mark(ra, masks, g.stream);
+        if (e == hipSuccess && marked) *marked = true;
+        return report(e, "router topk");
+    }
     return report(launch_route(ra, g.stream), "router topk");
 }
 
@@ -1178,6 +1185,10 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
     const size_t Tc = (size_t)(chunk < (int)n_tokens ? chunk : (int)n_tokens);
     const size_t S = Tc * n_used;
     const int max_tiles = (int)((S + 63) / 64) + (int)n_expert;
+    // routing writes the placement's bitmaps (4-token rows; the prefill chunk
+    // is a multiple of 32)
+    const bool mark = use_grouped && n_expert <= 256 && n_used <= 32 && Tc <= 2048 && Tc % 32 == 0 &&
+                      max_tiles <= 1280;
 
     Bump bp;
     const size_t o_xn = norm && !norm->xn ? bp.take(T * n_embd * 4) : 0;
@@ -1185,7 +1196,7 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
     const RouteScratch rs = route_scratch((int)T, n_embd, n_expert);
     const size_t o_w = bp.take(rs.bytes);
     size_t o_h = 0, o_t = 0, o_x16 = 0, o_cnt = 0, o_off = 0, o_ids = 0, o_wts = 0, o_pos = 0, o_tiles = 0, o_nt = 0,
-           o_h16 = 0, o_y = 0, o_rg = 0, o_rd = 0;
+           o_h16 = 0, o_y = 0, o_rg = 0, o_rd = 0, o_mask = 0;
     int rpi_gu = 0, rpi_dn = 0;
     if (use_grouped) {
         grouped_runs_per_tile((int)n_embd, (int)n_ff_exp, rpi_gu, rpi_dn);
@@ -1201,6 +1212,7 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
         o_rd = bp.take((size_t)max_tiles * rpi_dn * 4);
         o_h16 = bp.take(S * n_ff_exp * 2);
         o_y = bp.take(S * n_embd * 4);
+        if (mark) o_mask = bp.take((T + 3) / 4 * n_expert);
     } else {
         o_h = bp.take(T * n_used * n_ff_exp * 4);
         o_t = bp.take(T * n_used * n_ff_exp * 4);
@@ -1241,12 +1253,13 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
     }
     // the certified router only ahead of the decode kernels, which make its
     // weights exact (ExactTail / the fused selection)
-    bool x16_done = false;
+    bool x16_done = false, marked = false;
     DeferredSel sel;
     ExactTail xt{};
+    uint8_t *masks = mark ? ws + o_mask : nullptr;
     if (route_tokens(x, w_gate_inp, router_row_stride, router_type, (int)T, n_embd, n_expert, n_used, norm_topk_prob,
                      rb, &x16_done, !use_grouped, !use_grouped && gate_type == up_type ? &sel : nullptr,
-                     fuse_norm ? &np : nullptr, &xt) != 0)
+                     fuse_norm ? &np : nullptr, &xt, masks, &marked) != 0)
         return -1;
     if (fuse_norm) x = np.xn;
     ExpertWeights ew = make_ew(w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type, down_type, gate_row_stride,
@@ -1273,8 +1286,12 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
         hipError_t e = hipSuccess;
         {
             KScope ks("bucket");
-            e = launch_bucket(rb.idx + t0 * n_used, rb.scores + t0 * n_used, tc, (int)n_used, (int)n_expert, bo,
-                              g.stream);
+            if (marked)
+                e = launch_bucket_place(rb.idx + t0 * n_used, rb.scores + t0 * n_used, masks + t0 / 4 * n_expert, tc,
+                                        (int)n_used, (int)n_expert, bo, g.stream);
+            else
+                e = launch_bucket(rb.idx + t0 * n_used, rb.scores + t0 * n_used, tc, (int)n_used, (int)n_expert, bo,
+                                  g.stream);
         }
         if (e == hipSuccess) {
             KScope ks("moe_grouped_gate_up");

@@ -76,6 +76,71 @@ __host__ __device__ constexpr size_t bucket_stage_words(int chunks, int E)
     return (size_t)chunks * E + ((size_t)chunks * E + 1) / 2;
 }
 
+// Work items and run lists (every thread of the block calls it, after the
+// count scan): e = threadIdx.x, cnt = expert e's slot count, tb = its first
+// tile, ntile = its tiles, total_t = all tiles; xs: LDS scratch of
+// 3E words + max_tiles halfwords.  Per-expert tile facts go to xs: each
+// tile's expert, each expert's first tile, and for the run lists the tile
+// counts by cost class.
+__device__ void bucket_lists(int e, int cnt, int tb, int ntile, int total_t, int E, const BucketOut &o, int2 *wsum,
+                             uint32_t *xs)
+{
+    const int nt = total_t < o.max_tiles ? total_t : o.max_tiles;
+    int *tb_s = (int *)xs;                        // [E] first tile of each expert
+    uint32_t *info_s = xs + E;                    // [E] full tiles << 16 | m blocks of the last tile
+    uint32_t *cpos_s = info_s + E;                // [E] class-4 position << 16 | last tile's class position
+    uint16_t *own_s = (uint16_t *)(cpos_s + E);   // [nt] expert of each tile
+    if (e < E) {
+        tb_s[e] = tb;
+        for (int m = 0; m < ntile && tb + m < nt; m++) own_s[tb + m] = (uint16_t)e;
+    }
+    const bool runs = o.runs_gu != nullptr;
+    __syncthreads();                                      // wsum is read before the next scan writes it
+    if (runs) {
+        // run lists: (tile, n-run) for every tile, gate_up's and down's,
+        // heaviest first: tiles of 4 m blocks (16-token blocks), then 3, 2, 1,
+        // each class in tile order.  A run's cost grows with its m blocks,
+        // and the grouped kernels deal the list out round by round, so the
+        // rounds then hold runs of like cost.  Only an expert's last tile can
+        // have fewer than 4 m blocks.
+        const int full = cnt / o.tile_m, rest = cnt - full * o.tile_m;
+        const int mb_last = rest > 0 ? (4 * rest + o.tile_m - 1) / o.tile_m : 0;   // quarters of a tile: 1 .. 4
+        int a4 = e < E ? full + (mb_last == 4 ? 1 : 0) : 0, a3 = e < E && mb_last == 3 ? 1 : 0;
+        int a2 = e < E && mb_last == 2 ? 1 : 0, a1 = e < E && mb_last == 1 ? 1 : 0;
+        int n4 = 0, n3 = 0, n2 = 0, n1 = 0;
+        block_scan2(a4, a3, n4, n3, E, wsum);
+        __syncthreads();                                  // wsum is read before the next scan writes it
+        block_scan2(a2, a1, n2, n1, E, wsum);
+        if (e < E) {
+            // position among all tiles of this expert's first class-4 tile and of its last tile
+            const int last = mb_last == 4 || mb_last == 0 ? 0
+                           : mb_last == 3 ? n4 + a3 : mb_last == 2 ? n4 + n3 + a2 : n4 + n3 + n2 + a1;
+            info_s[e] = ((uint32_t)full << 16) | (uint32_t)mb_last;
+            cpos_s[e] = ((uint32_t)a4 << 16) | (uint32_t)last;
+        }
+    }
+    __syncthreads();
+    // One thread per tile (work item) writes its work item and runs.
+    for (int q = threadIdx.x; q < nt; q += BUCKET_TPB) {
+        const int lo = own_s[q], m = q - tb_s[lo];
+        o.tiles[q] = (lo << 16) | m;
+        if (runs) {
+            const uint32_t inf = info_s[lo], cp = cpos_s[lo];
+            const bool c4 = m < (int)(inf >> 16) || (inf & 0xffffu) == 4u;
+            const int pos = c4 ? (int)(cp >> 16) + m : (int)(cp & 0xffffu);
+            if (pos < o.max_tiles) {
+                for (int j = 0; j < o.rpi_gu; j++) o.runs_gu[pos * o.rpi_gu + j] = (q << 12) | j;
+                for (int j = 0; j < o.rpi_dn; j++) o.runs_dn[pos * o.rpi_dn + j] = (q << 12) | j;
+            }
+        }
+    }
+    if (runs && threadIdx.x == 0) {
+        o.n_runs[0] = nt * o.rpi_gu;
+        o.n_runs[1] = nt * o.rpi_dn;
+    }
+    __syncthreads();
+}
+
 __global__ void __launch_bounds__(BUCKET_TPB)
 k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int T, int k, int E, BucketOut o,
          int stage)
@@ -146,64 +211,7 @@ k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int 
         o.offsets[E] = total;
         *o.n_tiles = total_t < o.max_tiles ? total_t : o.max_tiles;
     }
-    // Per-expert tile facts in the staging area (free until the placement):
-    // each tile's expert, each expert's first tile, and for the run lists the
-    // tile counts by cost class.
-    const int nt = total_t < o.max_tiles ? total_t : o.max_tiles;
-    uint32_t *xs = sm + bucket_stage_words(chunks, E);
-    int *tb_s = (int *)xs;                        // [E] first tile of each expert
-    uint32_t *info_s = xs + E;                    // [E] full tiles << 16 | m blocks of the last tile
-    uint32_t *cpos_s = info_s + E;                // [E] class-4 position << 16 | last tile's class position
-    uint16_t *own_s = (uint16_t *)(cpos_s + E);   // [nt] expert of each tile
-    if (e < E) {
-        tb_s[e] = tb;
-        for (int m = 0; m < ntile && tb + m < nt; m++) own_s[tb + m] = (uint16_t)e;
-    }
-    const bool runs = o.runs_gu != nullptr;
-    __syncthreads();                                      // wsum is read before the next scan writes it
-    if (runs) {
-        // run lists: (tile, n-run) for every tile, gate_up's and down's,
-        // heaviest first: tiles of 4 m blocks (16-token blocks), then 3, 2, 1,
-        // each class in tile order.  A run's cost grows with its m blocks,
-        // and the grouped kernels deal the list out round by round, so the
-        // rounds then hold runs of like cost.  Only an expert's last tile can
-        // have fewer than 4 m blocks.
-        const int full = cnt / o.tile_m, rest = cnt - full * o.tile_m;
-        const int mb_last = rest > 0 ? (4 * rest + o.tile_m - 1) / o.tile_m : 0;   // quarters of a tile: 1 .. 4
-        int a4 = e < E ? full + (mb_last == 4 ? 1 : 0) : 0, a3 = e < E && mb_last == 3 ? 1 : 0;
-        int a2 = e < E && mb_last == 2 ? 1 : 0, a1 = e < E && mb_last == 1 ? 1 : 0;
-        int n4 = 0, n3 = 0, n2 = 0, n1 = 0;
-        block_scan2(a4, a3, n4, n3, E, wsum);
-        __syncthreads();                                  // wsum is read before the next scan writes it
-        block_scan2(a2, a1, n2, n1, E, wsum);
-        if (e < E) {
-            // position among all tiles of this expert's first class-4 tile and of its last tile
-            const int last = mb_last == 4 || mb_last == 0 ? 0
-                           : mb_last == 3 ? n4 + a3 : mb_last == 2 ? n4 + n3 + a2 : n4 + n3 + n2 + a1;
-            info_s[e] = ((uint32_t)full << 16) | (uint32_t)mb_last;
-            cpos_s[e] = ((uint32_t)a4 << 16) | (uint32_t)last;
-        }
-    }
-    __syncthreads();
-    // One thread per tile (work item) writes its work item and runs.
-    for (int q = threadIdx.x; q < nt; q += BUCKET_TPB) {
-        const int lo = own_s[q], m = q - tb_s[lo];
-        o.tiles[q] = (lo << 16) | m;
-        if (runs) {
-            const uint32_t inf = info_s[lo], cp = cpos_s[lo];
-            const bool c4 = m < (int)(inf >> 16) || (inf & 0xffffu) == 4u;
-            const int pos = c4 ? (int)(cp >> 16) + m : (int)(cp & 0xffffu);
-            if (pos < o.max_tiles) {
-                for (int j = 0; j < o.rpi_gu; j++) o.runs_gu[pos * o.rpi_gu + j] = (q << 12) | j;
-                for (int j = 0; j < o.rpi_dn; j++) o.runs_dn[pos * o.rpi_dn + j] = (q << 12) | j;
-            }
-        }
-    }
-    if (runs && threadIdx.x == 0) {
-        o.n_runs[0] = nt * o.rpi_gu;
-        o.n_runs[1] = nt * o.rpi_dn;
-    }
-    __syncthreads();
+    bucket_lists(e, cnt, tb, ntile, total_t, E, o, wsum, sm + bucket_stage_words(chunks, E));
     auto place = [&](int s, int ex, float sc) {
         const int t = s / k;
         if (ex < 0 || ex >= E) {          // out-of-range id: the slot is dropped
@@ -233,6 +241,119 @@ k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int 
             o.wts[p] = wts_l[p];
         }
     }
+}
+
+// Placement from the bitmaps k_route_mark writes: bit t % 4 of
+// masks[t / 4][e] is set when token t chose expert e; the 8 rows of a
+// 32-token chunk make k_bucket's 32-bit bitmap of that chunk, so the lists
+// come out in the same order.  Workgroup c places the slots of tokens 32c ..
+// 32c+31: every workgroup sums the bit counts of all chunks per expert (the
+// totals, and the part before its chunk), scans the totals for the offsets
+// and writes its own slots' token ids, weights and positions; workgroup 0
+// also writes counts, offsets, work items and run lists.  T <= PLACE_MAX_T,
+// k <= 32, E <= PLACE_MAX_E.
+constexpr int PLACE_MAX_T = 2048;
+constexpr int PLACE_MAX_E = 256;
+constexpr int PLACE_MAX_TILES = PLACE_MAX_T * 32 / 64 + PLACE_MAX_E;
+
+// The 32-bit bitmap of chunk c for expert e from its 8 rows of 4-token bytes
+// (rows past the last token are not read).
+__device__ __forceinline__ uint32_t place_mask(const uint8_t *rowsb, int c, int e, int E, int rows)
+{
+    uint32_t m = 0u;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int r = 8 * c + i;
+        if (r < rows) m |= (uint32_t)rowsb[r * E + e] << (4 * i);
+    }
+    return m;
+}
+
+__global__ void __launch_bounds__(BUCKET_TPB)
+k_bucket_place(const int32_t *__restrict__ idx, const float *__restrict__ scores, const uint8_t *__restrict__ masks,
+               int T, int k, int E, BucketOut o)
+{
+    __shared__ int32_t part_s[2][BUCKET_TPB];      // partial counts per (thread group, expert): all chunks, earlier chunks
+    __shared__ int32_t off_s[PLACE_MAX_E], pre_s[PLACE_MAX_E];
+    __shared__ uint32_t own_s[PLACE_MAX_E];       // this chunk's bitmaps
+    __shared__ int2 wsum[BUCKET_TPB / WAVE];
+    __shared__ uint32_t xs[3 * PLACE_MAX_E + (PLACE_MAX_TILES + 1) / 2];
+    __shared__ __attribute__((aligned(16))) uint8_t rowsb[PLACE_MAX_T / 4 * PLACE_MAX_E];   // all rows of the call
+    const int c = blockIdx.x, chunks = (T + 31) / 32, rows = (T + 3) / 4;
+    {
+        // every row into LDS at once: 16-byte loads (masks 16-byte aligned), the tail by bytes
+        const int nb = rows * E, n16 = nb / 16;
+        for (int i = threadIdx.x; i < n16; i += BUCKET_TPB) ((uint4 *)rowsb)[i] = ((const uint4 *)masks)[i];
+        for (int i = 16 * n16 + (int)threadIdx.x; i < nb; i += BUCKET_TPB) rowsb[i] = masks[i];
+    }
+    __syncthreads();
+    {
+        // G threads per expert, each over a run of consecutive chunks
+        const int G = BUCKET_TPB / E, gi = threadIdx.x / E, ei = threadIdx.x - gi * E;
+        const int L = (chunks + G - 1) / G, c0 = gi * L, c1 = min(chunks, c0 + L);
+        int tot = 0, before = 0;
+        if (gi < G)
+            for (int cc = c0; cc < c1; cc++) {
+                const int n = __popc(place_mask(rowsb, cc, ei, E, rows));
+                tot += n;
+                if (cc < c) before += n;
+            }
+        part_s[0][threadIdx.x] = tot;
+        part_s[1][threadIdx.x] = before;
+        if ((int)threadIdx.x < E) own_s[threadIdx.x] = place_mask(rowsb, c, threadIdx.x, E, rows);
+    }
+    __syncthreads();
+    const int e = threadIdx.x;
+    int cnt = 0, pc = 0;
+    if (e < E)
+        for (int g = 0; g < BUCKET_TPB / E; g++) {
+            cnt += part_s[0][g * E + e];
+            pc += part_s[1][g * E + e];
+        }
+    int off = cnt, tb = (cnt + o.tile_m - 1) / o.tile_m, total = 0, total_t = 0;
+    const int ntile = tb;
+    block_scan2(off, tb, total, total_t, E, wsum);
+    if (e < E) {
+        off_s[e] = off;
+        pre_s[e] = pc;
+    }
+    if (c == 0) {                                         // uniform over the workgroup
+        if (e < E) {
+            o.counts[e] = cnt;
+            o.offsets[e] = off;
+        }
+        if (threadIdx.x == 0) {
+            o.offsets[E] = total;
+            *o.n_tiles = total_t < o.max_tiles ? total_t : o.max_tiles;
+        }
+        bucket_lists(e, cnt, tb, ntile, total_t, E, o, wsum, xs);   // its barriers also publish off_s, pre_s
+    } else {
+        __syncthreads();
+    }
+    // this chunk's slots, one per thread
+    const int s = c * 32 * k + (int)threadIdx.x;
+    if ((int)threadIdx.x < 32 * k && s < T * k) {
+        const int t = s / k, ex = idx[s];
+        if (ex < 0 || ex >= E) {                          // out-of-range id: the slot is dropped
+            o.slot_pos[s] = -1;
+        } else {
+            const int pos = off_s[ex] + pre_s[ex] + __popc(own_s[ex] & ((1u << (t & 31)) - 1u));
+            o.ids[pos] = t;
+            o.wts[pos] = scores[s];
+            o.slot_pos[s] = pos;
+        }
+    }
+}
+
+hipError_t launch_bucket_place(const int32_t *idx, const float *scores, const uint8_t *masks, int T, int k, int E,
+                               const BucketOut &o, hipStream_t s)
+{
+    if (T <= 0 || T > PLACE_MAX_T || k <= 0 || k > 32 || E <= 0 || E > PLACE_MAX_E || o.max_tiles < 0 ||
+        o.max_tiles > PLACE_MAX_TILES || ((uintptr_t)masks & 15) != 0)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_bucket_place, dim3((unsigned)((T + 31) / 32)), dim3(BUCKET_TPB), 0, s, idx, scores, masks, T,
+                       k, E, o);
+    return hipGetLastError();
 }
 
 hipError_t launch_bucket(const int32_t *idx, const float *scores, int T, int k, int E, const BucketOut &o,

@@ -41,6 +41,10 @@ struct RouteArgs {
     bool norm;
 };
 hipError_t launch_route(const RouteArgs &a, hipStream_t s);
+// launch_route plus the bucketing bitmaps of launch_bucket_place: bit t % 4
+// of masks[t / 4][e] (rows of E bytes) is set when token t chose expert e.
+// E <= 256, k <= 32.
+hipError_t launch_route_mark(const RouteArgs &a, uint8_t *masks, hipStream_t s);
 
 // Router logits in the reference's order: logits[t][e] (row stride ldl) =
 // x[t][0]*W[e][0] + x[t][1]*W[e][1] + ... summed left to right with every
@@ -160,6 +164,11 @@ struct BucketOut {
 };
 hipError_t launch_bucket(const int32_t *idx, const float *scores, int T, int k, int E,
                          const BucketOut &o, hipStream_t s);
+// The same lists from launch_route_mark's bitmaps (the rows of these T
+// tokens), one workgroup per 32 tokens.  T <= 2048, k <= 32, E <= 256,
+// max_tiles <= 1280.
+hipError_t launch_bucket_place(const int32_t *idx, const float *scores, const uint8_t *masks, int T, int k, int E,
+                               const BucketOut &o, hipStream_t s);
 
 // Prefill grouped products (fp16 MFMA, fp32 accumulate).
 hipError_t launch_to_f16(const float *x, _Float16 *y, int64_t n, hipStream_t s);

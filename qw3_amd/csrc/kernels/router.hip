@@ -512,6 +512,36 @@ __global__ void __launch_bounds__(256) k_route(RouteArgs a)
     route_token(a, t, lane);
 }
 
+// k_route for the grouped path, with the bucketing bitmaps: workgroup q
+// routes tokens 4q .. 4q+3 (one per wave, as k_route) and writes its own row
+// q of masks, one byte per expert: bit t % 4 of masks[t / 4][e] is set when
+// token t chose expert e.  Rows are whole and private to their workgroup.
+__global__ void __launch_bounds__(256) k_route_mark(RouteArgs a, uint8_t *__restrict__ masks)
+{
+    __shared__ uint32_t m_l[ROUTE_MAX_E];
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    for (int e = threadIdx.x; e < a.E; e += blockDim.x) m_l[e] = 0u;
+    __syncthreads();
+    const int t = blockIdx.x * 4 + wave;
+    if (t < a.T) {                                        // uniform over the wave
+        route_token(a, t, lane);
+        if (lane < a.k) {
+            const int e = a.idx[(int64_t)t * a.out_stride + lane];   // this lane's own store
+            if (e >= 0 && e < a.E) atomicOr(&m_l[e], 1u << (t & 3));
+        }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < a.E; e += blockDim.x) masks[(int64_t)blockIdx.x * a.E + e] = (uint8_t)m_l[e];
+}
+
+hipError_t launch_route_mark(const RouteArgs &a, uint8_t *masks, hipStream_t s)
+{
+    if (a.T <= 0 || a.E <= 0 || a.E > ROUTE_MAX_E || a.k <= 0 || a.k > ROUTE_MAX_K || a.k > a.E)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_route_mark, dim3((unsigned)((a.T + 3) / 4)), dim3(256), 0, s, a, masks);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Certified router kernels (method and bound: route_select.h).
 // ---------------------------------------------------------------------------
