@@ -73,8 +73,9 @@ k_router_rows_f32(const uint8_t *__restrict__ rw, uint64_t rstride, int E, int K
 // while one is summed.  Rows are padded to 260 floats: the 16 lanes of each
 // ds_read_b128 pass read 16 different W rows (16 different bank groups).  x
 // is read one element per lane per 16-element block and reaches the other
-// lanes of its 16-lane row by DPP broadcast (rs_sum).  With x16 != nullptr the workgroups of expert
-// group 0 also write the fp16 copy of x that the grouped products read.
+// lanes of its 16-lane row by DPP broadcast (rs_sum).  With x16 != nullptr the workgroups also
+// write the fp16 copy of x that the grouped products read (spread over the expert groups when
+// the whole grid is resident at once).
 // DW: DMA width in bytes, 16 (rows 16-byte aligned, K % 4 == 0) or 4.
 // ---------------------------------------------------------------------------
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -236,7 +237,11 @@ k_router_seq(const float *__restrict__ x, int T, int K, int E, const float *__re
     const uint32_t w_off = (uint32_t)((lane & 15) * RS_ROWB);
     const uint32_t x_off = (uint32_t)((16 + 4 * wave + (lane >> 4)) * RS_ROWB);
     const uint32_t xl_off = x_off + 4u * (uint32_t)(lane & 15);      // this lane's element of each x block
-    const bool put16 = x16 != nullptr && blockIdx.y == 0;
+    // the fp16 copy of x: with one round of workgroups (D = 4, the whole grid
+    // resident) chunk c by the expert group c mod gridDim.y, so the
+    // conversion is spread over every workgroup of the token group; with
+    // several rounds all of it by expert group 0 (measured faster there)
+    const bool put16_any = x16 != nullptr;
 
 #pragma unroll
     for (int c = 0; c < D - 1; c++)
@@ -276,7 +281,7 @@ k_router_seq(const float *__restrict__ x, int T, int K, int E, const float *__re
                 acc = acc + __uint_as_float(xv) * __uint_as_float(wv);
             }
         }
-        if (put16) {
+        if (put16_any && (D >= 4 ? c % (int)gridDim.y == (int)blockIdx.y : blockIdx.y == 0)) {
             // thread: x row tid / 16 of the stage, 16 floats at 16 * (tid % 16)
             const int t = t0 + (tid >> 4), k0 = c * RS_CH + 16 * (tid & 15);
             if (t < T && k0 < K) {
