@@ -376,6 +376,23 @@ def test_prefill_hot_experts(hip_ready):
     assert_close(got, want)
 
 
+@pytest.mark.parametrize("E,k,T", [(32, 4, 16), (48, 8, 77), (64, 6, 101), (256, 16, 300)])
+def test_prefill_expert_counts(hip_ready, E, k, T):
+    """Grouped path (routing with its 4-token expert bitmaps, the parallel
+    placement) at other expert counts and top-k widths than Qwen3's: E not
+    dividing the placement's 1024 threads (48), up to 256 experts and 16
+    slots per token (512 slots per 32-token workgroup), T not a multiple of
+    4 or 32."""
+    spec = W.LayerSpec(n_embd=1024, n_ff=256, n_expert=E)
+    case = Case(spec, seed=600 + E + k)
+    x = W.fill(W.NORMAL, 9, T, T * spec.n_embd, 0.0, 1.0).reshape(T, spec.n_embd)
+    print(f"  prefill E={E} k={k} T={T}", flush=True)
+    got, gi, _, _ = case.gpu_batch(x, n_used=k, prefill_min=1)
+    want, oi, _, probs = case.oracle(x, n_used=k)
+    assert index_mismatches(gi, oi, probs) == 0
+    assert_close(got, want)
+
+
 @pytest.mark.parametrize("T", [1, 4, 16, 64, 256, 1024])
 def test_q8_0_sweep_config5(hip_ready, q80, T):
     x = W.make_inputs(5, T, seed=104 + T)
