@@ -88,12 +88,15 @@ __device__ __forceinline__ void gg_dma_done()
 }
 
 // Q4_K blocks load as whole 16-byte vectors when the expert's rows are
-// 16-byte aligned (always in GGUF files); the other types load dwords.
+// 16-byte aligned (always in GGUF files); Q6_K blocks load their scales and d
+// in two loads when every block starts on an even byte (even base and row
+// stride: 210-byte blocks then sit at 0 or 2 mod 4); Q8_0 loads dwords.
 template <int TYPE>
 __device__ __forceinline__ bool gg_aligned(const uint8_t *a, const uint8_t *b, uint64_t stride)
 {
-    if constexpr (TYPE != T_Q4_K) return true;
-    return ((((uintptr_t)a) | ((uintptr_t)b) | stride) & 15) == 0;
+    if constexpr (TYPE == T_Q4_K) return ((((uintptr_t)a) | ((uintptr_t)b) | stride) & 15) == 0;
+    if constexpr (TYPE == T_Q6_K) return ((((uintptr_t)a) | ((uintptr_t)b) | stride) & 1) == 0;
+    return true;
 }
 
 // Weight stream: explicit loads and waits.  The weight loads are inline asm
@@ -184,6 +187,50 @@ template <> struct GgStage<T_Q4_K, false> {
         r.hdr = make_uint4(w[0][0], w[0][1], w[0][2], w[0][3]);
         r.q0 = make_uint4(w[1][0], w[1][1], w[1][2], w[1][3]);
         r.q1 = make_uint4(w[2][0], w[2][1], w[2][2], w[2][3]);
+    }
+};
+// Q6_K, blocks on even bytes: the two scale windows and d come from one
+// 16-byte load at the aligned address below the scales (offset 192) and one
+// dword at offset 208 from it, which holds d (block offset sh is 0 or 2) and
+// reads no further past the block than the 12-byte windows do.
+template <> struct GgStage<T_Q6_K, true> {
+    static constexpr int NLOAD = 8;
+    gg_u32x3 f[2][3];
+    gg_u32x4 sc;
+    uint32_t dd, sh;
+    __device__ __forceinline__ void issue(const uint8_t *blk, int g)
+    {
+        const uint8_t *b4 = (const uint8_t *)((uintptr_t)blk & ~(uintptr_t)3);
+        sh = (uint32_t)((uintptr_t)blk & 3);
+#pragma unroll
+        for (int hv = 0; hv < 2; hv++) {
+            const int off[3] = { 64 * hv + 8 * g, 64 * hv + 32 + 8 * g, 128 + 32 * hv + 8 * g };
+#pragma unroll
+            for (int fi = 0; fi < 3; fi++) gg_ldx3(f[hv][fi], b4 + off[fi]);
+        }
+        gg_ldx4(sc, b4 + 192);
+        gg_ldx1(dd, b4 + 208);
+    }
+    template <int N> __device__ __forceinline__ void wait()
+    {
+        asm volatile("s_waitcnt vmcnt(%8)" : "+v"(f[0][0]), "+v"(f[0][1]), "+v"(f[0][2]), "+v"(f[1][0]), "+v"(f[1][1]),
+                     "+v"(f[1][2]), "+v"(sc), "+v"(dd) : "n"(N));
+    }
+    __device__ __forceinline__ void to_raw(RawUnits<T_Q6_K> &r) const
+    {
+#pragma unroll
+        for (int hv = 0; hv < 2; hv++)
+#pragma unroll
+            for (int fi = 0; fi < 3; fi++) {
+                r.f[hv][fi][0] = f[hv][fi].x;
+                r.f[hv][fi][1] = f[hv][fi].y;
+                r.f[hv][fi][2] = f[hv][fi].z;
+            }
+        // the 12-byte scale windows at 192 and 200 from b4
+        r.f[0][3][0] = sc.x; r.f[0][3][1] = sc.y; r.f[0][3][2] = sc.z;
+        r.f[1][3][0] = sc.z; r.f[1][3][1] = sc.w; r.f[1][3][2] = dd;
+        r.dw = (dd >> (8 * sh)) & 0xffffu;
+        r.sh = sh;
     }
 };
 template <bool AL> struct GgStage<T_Q6_K, AL> {
