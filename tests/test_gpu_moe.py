@@ -240,12 +240,13 @@ def test_moe_ffn_router_logits(hip_ready, type_):
 @pytest.mark.parametrize("T,K,E,align", [(1, 2048, 128, 0), (2, 2048, 128, 0), (5, 2048, 128, 0),
                                          (17, 2048, 128, 0), (32, 1000, 72, 0), (37, 1000, 72, 0),
                                          (130, 2048, 128, 4), (1100, 512, 128, 0), (6, 1536, 200, 0),
-                                         (3, 4096, 256, 0)])
+                                         (3, 4096, 256, 0), (2050, 1024, 136, 0)])
 def test_route_logits_shapes(hip_ready, T, K, E, align, mode):
     """Both router kernels (products split off for T <= 32, one lane per
     chain above): ragged T (workgroup tails), K not a multiple of the chunk
     width (scalar tail), E not a multiple of 16, an x row start that is only
-    4-byte aligned (4-byte DMAs), and long batches (2-stage ring)."""
+    4-byte aligned (4-byte DMAs), and long batches (2-stage ring), also with
+    E not a multiple of 16."""
     rng = np.random.default_rng(T + K + E)
     wr = (rng.standard_normal((E, K)) * 0.02).astype(np.float32)
     x = rng.standard_normal((T, K)).astype(np.float32)
