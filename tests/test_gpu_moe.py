@@ -377,6 +377,38 @@ def test_prefill_hot_experts(hip_ready):
     assert_close(got, want)
 
 
+def test_prefill_unaligned_experts(hip_ready):
+    """Grouped path on expert tensors whose blocks miss the fast weight loads:
+    gate and up 4 bytes past a 16-byte boundary (Q4_K blocks read as dwords
+    and realigned), down at an odd byte (Q6_K scales and d in three loads
+    instead of two).  Same bytes as the oracle's."""
+    spec = W.LayerSpec(n_embd=1024, n_ff=256, n_expert=16)
+    case = Case(spec, seed=611)
+    h = case.host
+    keep = []
+
+    def placed(raw, off):
+        base = ds3.Buffer.from_array(np.concatenate([np.zeros(off, np.uint8), raw, np.zeros(64, np.uint8)]))
+        keep.append(base)
+        return base.view(off, raw.nbytes)
+
+    ex = ds3.ExpertTensors(placed(h.gate, 4), placed(h.up, 4), placed(h.down, 1), spec.gate_type, spec.up_type,
+                           spec.down_type, spec.n_embd, spec.n_ff)
+    T = 96
+    x = W.fill(W.NORMAL, 13, T, T * spec.n_embd, 0.0, 1.0).reshape(T, spec.n_embd)
+    out = ds3.Buffer.alloc(T * spec.n_embd * 4)
+    idx = ds3.Buffer.alloc(T * W.N_USED * 4)
+    prev = ds3.set_prefill_min_tokens(1)
+    try:
+        ds3.moe_ffn_batch(ds3.Buffer.from_array(x), case.dev.router, spec.router_type, ex, out, T, spec.n_expert,
+                          W.N_USED, indices=idx)
+    finally:
+        ds3.set_prefill_min_tokens(prev)
+    want, oi, _, probs = case.oracle(x)
+    assert index_mismatches(idx.read(np.int32, (T, W.N_USED)), oi, probs) == 0
+    assert_close(out.read(np.float32, (T, spec.n_embd)), want)
+
+
 @pytest.mark.parametrize("E,k,T", [(32, 4, 16), (48, 8, 77), (64, 6, 101), (256, 16, 300)])
 def test_prefill_expert_counts(hip_ready, E, k, T):
     """Grouped path (routing with its 4-token expert bitmaps, the parallel
