@@ -377,12 +377,14 @@ def test_prefill_hot_experts(hip_ready):
     assert_close(got, want)
 
 
-def test_prefill_unaligned_experts(hip_ready):
+@pytest.mark.parametrize("types,offs", [((12, 12, 14), (4, 4, 1)), ((8, 8, 8), (2, 2, 2))])
+def test_prefill_unaligned_experts(hip_ready, types, offs):
     """Grouped path on expert tensors whose blocks miss the fast weight loads:
-    gate and up 4 bytes past a 16-byte boundary (Q4_K blocks read as dwords
-    and realigned), down at an odd byte (Q6_K scales and d in three loads
-    instead of two).  Same bytes as the oracle's."""
-    spec = W.LayerSpec(n_embd=1024, n_ff=256, n_expert=16)
+    Q4_K gate and up 4 bytes past a 16-byte boundary (blocks read as dwords
+    and realigned), Q6_K down at an odd byte (scales and d in three loads
+    instead of two), Q8_0 rows 2 bytes off a dword (every block realigned).
+    Same bytes as the oracle's."""
+    spec = W.LayerSpec(*types, n_embd=1024, n_ff=256, n_expert=16)
     case = Case(spec, seed=611)
     h = case.host
     keep = []
@@ -392,8 +394,8 @@ def test_prefill_unaligned_experts(hip_ready):
         keep.append(base)
         return base.view(off, raw.nbytes)
 
-    ex = ds3.ExpertTensors(placed(h.gate, 4), placed(h.up, 4), placed(h.down, 1), spec.gate_type, spec.up_type,
-                           spec.down_type, spec.n_embd, spec.n_ff)
+    ex = ds3.ExpertTensors(placed(h.gate, offs[0]), placed(h.up, offs[1]), placed(h.down, offs[2]), spec.gate_type,
+                           spec.up_type, spec.down_type, spec.n_embd, spec.n_ff)
     T = 96
     x = W.fill(W.NORMAL, 13, T, T * spec.n_embd, 0.0, 1.0).reshape(T, spec.n_embd)
     out = ds3.Buffer.alloc(T * spec.n_embd * 4)
