@@ -299,6 +299,24 @@ int ds3_hip_set_router_mode(int mode);
  * sums for some candidates) since init or the last reset; synchronises. */
 int ds3_hip_router_stats(uint64_t *certified, uint64_t *repaired, int reset);
 
+/* Test hook (no ds3_metal.h counterpart): the bucketing lists the grouped
+ * path of ds3_hip_moe_ffn_batch / _noalloc / ds3_hip_moe_block built on the
+ * device for the last chunk of its last call -- the lists the reference's
+ * host loop builds (src/ds3_engine.c:932-965) plus the grouped kernels' work
+ * items and run lists.  Call it before any other library call that may reuse
+ * the workspace; synchronises.  meta[DS3_HIP_LISTS_META] = { chunk's first
+ * token, chunk's tokens tc, n_used k, n_expert E, work items n_tiles,
+ * gate_up runs, down runs, 1 if the lists came from the routing's bitmaps
+ * (else from the routed indices), gate_up runs per work item, down runs per
+ * work item, max work items, tokens per work item }.  Each array not NULL
+ * receives: counts[E], offsets[E + 1], ids / wts / slot_pos[tc * k],
+ * tiles[n_tiles], runs_gu / runs_dn[their counts].  Work item = expert << 16
+ * | token tile; run = work item index << 12 | n run.  -1 when no grouped call
+ * ran since the workspace last moved. */
+#define DS3_HIP_LISTS_META 12
+int ds3_hip_debug_grouped_lists(int32_t *meta, int32_t *counts, int32_t *offsets, int32_t *ids, float *wts,
+                                int32_t *slot_pos, int32_t *tiles, int32_t *runs_gu, int32_t *runs_dn);
+
 /* ds3_hip_moe_ffn_batch uses the grouped (prefill) path when
  * n_tokens >= min_tokens, the per-token GEMV path otherwise.  0 restores the
  * default.  Returns the previous value. */

@@ -91,6 +91,15 @@ struct State {
     std::vector<double> stat_ms;
     bool stats_dirty = true;
     hipEvent_t t0 = nullptr, t1 = nullptr;
+    // The bucketing lists of the last chunk of the last grouped-path call
+    // (device pointers into that call's workspace), for
+    // ds3_hip_debug_grouped_lists; cleared when the workspace moves.
+    struct {
+        bool valid = false;
+        ds3k::BucketOut bo{};
+        int t0 = 0, tc = 0, k = 0, E = 0;
+        bool marked = false;
+    } lists;
 };
 
 State g;
@@ -144,6 +153,7 @@ uint8_t *ws_get(size_t bytes)
                         "before ds3_hip_graph_begin\n", bytes, g.ws_bytes);
         return nullptr;
     }
+    g.lists.valid = false;
     if (g.ws) {
         (void)hipStreamSynchronize(g.stream);
         if (g.graphs.empty()) (void)hipFree(g.ws);
@@ -265,6 +275,41 @@ bool fits(const ds3_hip_buffer_t *b, size_t need, const char *what)
         return false;
     }
     return true;
+}
+
+// Bytes a [rows] x row_bytes matrix with rows `stride` bytes apart spans.
+uint64_t span_bytes(uint64_t rows, uint64_t stride, uint64_t row_b)
+{
+    return rows == 0 ? 0 : (rows - 1) * stride + row_b;
+}
+
+// The router and the routed experts' tensors hold what a MoE call reads on
+// the device: row strides of at least one row's bytes, n_expert router rows,
+// n_expert experts per tensor (expert e at e * rows * stride when no offset
+// table is given) and, with a table, its n_expert x 3 u64 entries.  The
+// table's offsets themselves live in device memory and are the caller's, as
+// the engine builds them (src/ds3_engine.c:1747-1773).
+bool moe_weights_fit(const ds3_hip_buffer_t *router, uint64_t rstride, int rtype, const ds3_hip_buffer_t *wg,
+                     const ds3_hip_buffer_t *wu, const ds3_hip_buffer_t *wd, int gt, int ut, int dt, uint64_t gs,
+                     uint64_t us, uint64_t ds, const ds3_hip_buffer_t *table, uint32_t n_embd, uint32_t n_expert,
+                     uint32_t n_ff)
+{
+    const uint64_t rb_r = row_bytes(rtype, n_embd), rb_g = row_bytes(gt, n_embd), rb_u = row_bytes(ut, n_embd),
+                   rb_d = row_bytes(dt, n_ff);
+    struct { const char *name; uint64_t stride, need; } st[4] = {
+        { "router_row_stride", rstride, rb_r }, { "gate_row_stride", gs, rb_g },
+        { "up_row_stride", us, rb_u }, { "down_row_stride", ds, rb_d } };
+    for (const auto &s : st)
+        if (s.need == 0 || s.stride < s.need) {
+            fprintf(stderr, "ds3_hip: %s=%llu is shorter than one row (%llu bytes)\n", s.name,
+                    (unsigned long long)s.stride, (unsigned long long)s.need);
+            return false;
+        }
+    if (!fits(router, span_bytes(n_expert, rstride, rb_r), "router (n_expert rows)")) return false;
+    if (table) return fits(table, (size_t)n_expert * 3 * sizeof(uint64_t), "expert_offsets (n_expert x 3 u64)");
+    return fits(wg, span_bytes((uint64_t)n_expert * n_ff, gs, rb_g), "gate experts (n_expert x n_ff rows)") &&
+           fits(wu, span_bytes((uint64_t)n_expert * n_ff, us, rb_u), "up experts (n_expert x n_ff rows)") &&
+           fits(wd, span_bytes((uint64_t)n_expert * n_embd, ds, rb_d), "down experts (n_expert x n_embd rows)");
 }
 
 // A certified selection left to the decode gate/up kernel's prologue
@@ -910,6 +955,23 @@ extern "C" int ds3_hip_moe_ffn(
     if (!fits(input, (size_t)n_embd * 4, "input") || !fits(output, (size_t)n_embd * 4, "output") ||
         !fits(gate_logits, (size_t)n_expert * 4, "gate_logits"))
         return -1;
+    if (!moe_weights_fit(w_gate_inp, router_row_stride, router_type, w_gate_exps, w_up_exps, w_down_exps, gate_type,
+                         up_type, down_type, gate_row_stride, up_row_stride, down_row_stride, expert_offsets, n_embd,
+                         n_expert, n_ff_exp))
+        return -1;
+    if (has_shared &&
+        (!fits(w_shared_gate, span_bytes(n_ff_shared, shared_gate_row_stride, row_bytes(shared_gate_type, n_embd)),
+               "shared_gate") ||
+         !fits(w_shared_up, span_bytes(n_ff_shared, shared_up_row_stride, row_bytes(shared_up_type, n_embd)),
+               "shared_up") ||
+         !fits(w_shared_down, span_bytes(n_embd, shared_down_row_stride, row_bytes(shared_down_type, n_ff_shared)),
+               "shared_down") ||
+         shared_gate_row_stride < row_bytes(shared_gate_type, n_embd) ||
+         shared_up_row_stride < row_bytes(shared_up_type, n_embd) ||
+         shared_down_row_stride < row_bytes(shared_down_type, n_ff_shared))) {
+        fprintf(stderr, "ds3_hip: moe_ffn: shared expert weights smaller than their shapes\n");
+        return -1;
+    }
 
     const uint32_t ff_max = has_shared && n_ff_shared > n_ff_exp ? n_ff_shared : n_ff_exp;
     Bump bp;
@@ -1176,6 +1238,10 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
         fprintf(stderr, "ds3_hip: router type %d unsupported\n", router_type);
         return -1;
     }
+    if (!moe_weights_fit(w_gate_inp, router_row_stride, router_type, w_gate_exps, w_up_exps, w_down_exps, gate_type,
+                         up_type, down_type, gate_row_stride, up_row_stride, down_row_stride, expert_offsets, n_embd,
+                         n_expert, n_ff_exp))
+        return -1;
     const size_t T = n_tokens;
 
     const bool grouped_ok = gate_type == up_type && grouped_type_ok(gate_type, (int)n_embd) &&
@@ -1185,10 +1251,12 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
     const size_t Tc = (size_t)(chunk < (int)n_tokens ? chunk : (int)n_tokens);
     const size_t S = Tc * n_used;
     const int max_tiles = (int)((S + 63) / 64) + (int)n_expert;
-    // routing writes the placement's bitmaps (4-token rows; the prefill chunk
-    // is a multiple of 32)
-    const bool mark = use_grouped && n_expert <= 256 && n_used <= 32 && Tc <= 2048 && Tc % 32 == 0 &&
-                      max_tiles <= 1280;
+    // routing writes the placement's bitmaps (4-token rows).  A call of more
+    // than one chunk places chunk by chunk: the chunk must then be a multiple
+    // of 32 tokens, and every chunk's slice of the bitmaps must start on 16
+    // bytes, as the placement loads them.
+    const bool mark = use_grouped && n_expert <= 256 && n_used <= 32 && Tc <= 2048 && max_tiles <= 1280 &&
+                      (T <= Tc || (Tc % 32 == 0 && (Tc / 4 * n_expert) % 16 == 0));
 
     Bump bp;
     const size_t o_xn = norm && !norm->xn ? bp.take(T * n_embd * 4) : 0;
@@ -1262,6 +1330,14 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
                      fuse_norm ? &np : nullptr, &xt, masks, &marked) != 0)
         return -1;
     if (fuse_norm) x = np.xn;
+    if (use_grouped && xt.w != nullptr) {
+        // certified routing on the grouped path (router mode 2): the weights
+        // from the exact logits of the selected experts, as the decode path's
+        // gate/up launch computes them
+        KScope ks("exact_weights");
+        const hipError_t e = launch_exact_weights(x, n_embd, xt, (int)n_embd, g.stream);
+        if (e != hipSuccess) return report(e, what);
+    }
     ExpertWeights ew = make_ew(w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type, down_type, gate_row_stride,
                                up_row_stride, down_row_stride, expert_offsets);
     if (!use_grouped) {
@@ -1292,6 +1368,15 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
             else
                 e = launch_bucket(rb.idx + t0 * n_used, rb.scores + t0 * n_used, tc, (int)n_used, (int)n_expert, bo,
                                   g.stream);
+        }
+        if (e == hipSuccess) {
+            g.lists.valid = true;
+            g.lists.bo = bo;
+            g.lists.t0 = (int)t0;
+            g.lists.tc = tc;
+            g.lists.k = (int)n_used;
+            g.lists.E = (int)n_expert;
+            g.lists.marked = marked;
         }
         if (e == hipSuccess) {
             KScope ks("moe_grouped_gate_up");
@@ -1422,6 +1507,35 @@ extern "C" int ds3_hip_dequantize(const ds3_hip_buffer_t *src, uint64_t src_offs
     if (!fits(src, src_offset + n / blk * bytes, "src") || !fits(dst, n * 4, "dst")) return -1;
     KScope ks("dequant");
     return finish(launch_dequant(type, cptr(src) + src_offset, fptr(dst), (int64_t)n, g.stream), "dequantize");
+}
+
+extern "C" int ds3_hip_debug_grouped_lists(int32_t *meta, int32_t *counts, int32_t *offsets, int32_t *ids,
+                                           float *wts, int32_t *slot_pos, int32_t *tiles, int32_t *runs_gu,
+                                           int32_t *runs_dn)
+{
+    if (!meta || refuse_in_capture("debug_grouped_lists") || !ensure_init()) return -1;
+    if (!g.lists.valid) {
+        fprintf(stderr, "ds3_hip: debug_grouped_lists: no grouped-path call since the workspace last moved\n");
+        return -1;
+    }
+    const BucketOut &o = g.lists.bo;
+    int32_t n[3] = { 0, 0, 0 };
+    if (hipStreamSynchronize(g.stream) != hipSuccess ||
+        hipMemcpy(&n[0], o.n_tiles, 4, hipMemcpyDeviceToHost) != hipSuccess ||
+        hipMemcpy(&n[1], o.n_runs, 8, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    const int E = g.lists.E, S = g.lists.tc * g.lists.k;
+    const int32_t m[DS3_HIP_LISTS_META] = { g.lists.t0, g.lists.tc, g.lists.k, E, n[0], n[1], n[2],
+                                            g.lists.marked ? 1 : 0, o.rpi_gu, o.rpi_dn, o.max_tiles, o.tile_m };
+    memcpy(meta, m, sizeof m);
+    struct { void *dst; const void *src; size_t bytes; } cp[] = {
+        { counts, o.counts, (size_t)E * 4 }, { offsets, o.offsets, ((size_t)E + 1) * 4 },
+        { ids, o.ids, (size_t)S * 4 }, { wts, o.wts, (size_t)S * 4 }, { slot_pos, o.slot_pos, (size_t)S * 4 },
+        { tiles, o.tiles, (size_t)n[0] * 4 }, { runs_gu, o.runs_gu, (size_t)n[1] * 4 },
+        { runs_dn, o.runs_dn, (size_t)n[2] * 4 } };
+    for (const auto &c : cp)
+        if (c.dst && c.bytes && hipMemcpy(c.dst, c.src, c.bytes, hipMemcpyDeviceToHost) != hipSuccess) return -1;
+    return 0;
 }
 
 extern "C" int ds3_hip_router_stats(uint64_t *certified, uint64_t *repaired, int reset)

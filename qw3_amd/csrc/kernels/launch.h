@@ -119,6 +119,12 @@ struct ExactTail {
     RouteArgs ra;
 };
 
+// The same exact weights as a launch of its own (one workgroup per token of
+// xt.ra), for tokens routed by the certified selection launch that no decode
+// gate/up launch follows; x: the rows the router summed, ldx floats apart,
+// 16-byte aligned.
+hipError_t launch_exact_weights(const float *x, int64_t ldx, const ExactTail &xt, int K, hipStream_t s);
+
 // Decode (small T) expert products.
 //   h[slot][F] = silu(x[t] . Wg_e) * (x[t] . Wu_e), slot = t*n_used + k, e = idx[slot]
 // With xt, also the exact weights of the tokens (xt->ra.idx == idx).

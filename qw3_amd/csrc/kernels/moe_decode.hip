@@ -100,6 +100,23 @@ k_decode_gate_up(const float *__restrict__ x, int64_t ldx, const int32_t *__rest
                                    which, h);
 }
 
+// The exact-weights stage on its own, one workgroup per token: token t's
+// weights from the reference's exact logits of its selected experts (the
+// routing of the certified router's selection launch), for callers that run
+// no decode gate/up launch after it (the grouped prefill path).
+__global__ void __launch_bounds__(DEC_TPB)
+k_exact_weights(const float *__restrict__ x, int64_t ldx, ExactTail xt, int K)
+{
+    extern __shared__ __attribute__((aligned(16))) float xw_lds[];   // exact_chain_lds(K) bytes
+    const int t = blockIdx.x, wave = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
+    float4 xv[4];
+    exact_load_x(x + (int64_t)t * ldx, K, xv, threadIdx.x);
+    const int e_lane = lane < xt.ra.k ? xt.ra.idx[(int64_t)t * xt.ra.out_stride + lane] : 0;
+    exact_store_x(xw_lds, K, xv, threadIdx.x);
+    __syncthreads();                                             // the row is in LDS
+    exact_weights_wg(xw_lds, K, xt.w, xt.wstride, xt.ra, t, e_lane, wave, lane);
+}
+
 // Warm each XCD's L2 with the down rows its down workgroups will read:
 // workgroups go round-robin to the 8 XCDs in dispatch order, so down
 // workgroup x (rows 8x .. 8x+7 of every selected expert, one token) runs on
@@ -420,6 +437,15 @@ hipError_t launch_decode_gate_up_sel(const float *x, int T, int n_used, const Ex
     const size_t lds = std::max((size_t)cs.ca.nb * (K + 4) * sizeof(float), exact_chain_lds(K));
     DS3_T_SWITCH(ew.gate_type, DS3_G_SWITCH(G, DS3_U_SWITCH(UPL, hipLaunchKernelGGL(
         (k_decode_gate_up_sel<TV, GV, UV>), grid, dim3(DEC_TPB), lds, s, x, n_used, ew, K, F, h, nx, cs, ra))));
+    return hipGetLastError();
+}
+
+hipError_t launch_exact_weights(const float *x, int64_t ldx, const ExactTail &xt, int K, hipStream_t s)
+{
+    if (xt.w == nullptr || xt.ra.T <= 0 || !exact_tail_ok(&xt, xt.ra.T * xt.ra.k, xt.ra.k, K) || ldx % 4 != 0 ||
+        ((uintptr_t)x & 15) != 0)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_exact_weights, dim3((unsigned)xt.ra.T), dim3(DEC_TPB), exact_chain_lds(K), s, x, ldx, xt, K);
     return hipGetLastError();
 }
 

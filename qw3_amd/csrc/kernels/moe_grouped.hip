@@ -370,6 +370,19 @@ __device__ __forceinline__ void gg_step(const RawUnits<TYPE> (&raw)[NB], uint32_
     }
 }
 
+// A K loop leaves D - 1 weight stages loading past its last step (every
+// stage is issued unconditionally).  Wait for them before the loop returns,
+// naming every register of every stage, so no later code can be given a
+// register that a late load still writes.
+template <int D, int NB, class St>
+__device__ __forceinline__ void gg_ring_drain(St (&ring)[D][NB])
+{
+#pragma unroll
+    for (int d = 0; d < D; d++)
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) ring[d][nb].template wait<0>();
+}
+
 // The K loop of a run: U = nnt * S steps (n tile t = u / S, K step u % S),
 // weights of step u + D - 1 loaded while step u is decoded; after the last K
 // step of an n tile the epilogue stores it.  rows[nb]: this lane's weight row
@@ -436,6 +449,7 @@ __device__ __forceinline__ void gg_run(const uint8_t *const (&rows)[NB], uint64_
             }
         }
     }
+    gg_ring_drain<D, NB>(ring);
 }
 
 // gate_up's K loop: activation rows stream through two LDS chunk buffers of
@@ -532,6 +546,8 @@ __device__ __forceinline__ void gg_run_chunked(const uint8_t *const (&rows)[2], 
 #pragma unroll
             for (int j = 0; j < NB; j++) acc[i][j] = floatx4{ 0.f, 0.f, 0.f, 0.f };
     }
+    gg_ring_drain<D, NB>(ring);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");     // the last chunk DMA (a_src) has landed too
 }
 
 // This lane's byte offsets of the 8 K-slots in a step's activation slice.

@@ -252,6 +252,24 @@ def router_stats(reset: bool = False) -> tuple[int, int]:
     return c.value, r.value
 
 
+def grouped_lists() -> dict:
+    """The bucketing lists of the last chunk of the last grouped-path call
+    (ds3_hip_debug_grouped_lists), as numpy arrays."""
+    h = hip()
+    meta = np.zeros(12, np.int32)
+    _check(h.ds3_hip_debug_grouped_lists(meta.ctypes.data, *([None] * 8)), "debug_grouped_lists")
+    t0, tc, k, E, nt, ngu, ndn, marked, rpi_gu, rpi_dn, max_tiles, tile_m = (int(v) for v in meta)
+    S = tc * k
+    a = {"counts": np.zeros(E, np.int32), "offsets": np.zeros(E + 1, np.int32), "ids": np.zeros(S, np.int32),
+         "wts": np.zeros(S, np.float32), "slot_pos": np.zeros(S, np.int32), "tiles": np.zeros(nt, np.int32),
+         "runs_gu": np.zeros(ngu, np.int32), "runs_dn": np.zeros(ndn, np.int32)}
+    _check(h.ds3_hip_debug_grouped_lists(meta.ctypes.data, *(v.ctypes.data for v in a.values())),
+           "debug_grouped_lists")
+    a.update(t0=t0, tc=tc, k=k, E=E, marked=bool(marked), rpi_gu=rpi_gu, rpi_dn=rpi_dn, max_tiles=max_tiles,
+             tile_m=tile_m)
+    return a
+
+
 def device_info() -> dict:
     arch = C.create_string_buffer(64)
     ncu = C.c_int()

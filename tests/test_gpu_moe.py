@@ -307,6 +307,92 @@ def test_bucket_matches_oracle(hip_ready, T):
     assert np.array_equal(ids, oids) and np.array_equal(wts, owts) and np.array_equal(pos, opos)
 
 
+def check_lists(L: dict, idx: np.ndarray, sc: np.ndarray):
+    """The grouped path's lists for one chunk (ds3.grouped_lists) against the
+    oracle's bucketing of the same routing (reference src/ds3_engine.c:932-955:
+    counts, offsets, token ids and weights in token order per expert, the
+    position of every slot), bit for bit; then its work items (every expert's
+    tiles of tile_m positions in expert order) and run lists (every work item
+    once per n run, heaviest first: items of 4 m blocks of 16 tokens, then 3,
+    2, 1, each class in item order)."""
+    E, k, tile_m = L["E"], L["k"], L["tile_m"]
+    t0, tc = L["t0"], L["tc"]
+    ci, cs = idx[t0:t0 + tc], sc[t0:t0 + tc]
+    oc, oo, oids, owts, opos = O.bucket(ci, cs, E)
+    assert np.array_equal(L["counts"], oc)
+    assert np.array_equal(L["offsets"][:E], oo) and L["offsets"][E] == tc * k
+    assert np.array_equal(L["ids"], oids)
+    assert np.array_equal(L["wts"].view(np.uint32), owts.view(np.uint32))
+    assert np.array_equal(L["slot_pos"], opos)
+    want_tiles = [(e << 16) | m for e in range(E) for m in range((int(oc[e]) + tile_m - 1) // tile_m)]
+    assert L["tiles"].tolist() == want_tiles
+    mb = []                                       # 16-token m blocks of each work item
+    for q in want_tiles:
+        e, m = q >> 16, q & 0xFFFF
+        mb.append((min(tile_m, int(oc[e]) - m * tile_m) + 15) // 16)
+    order = [q for c in (4, 3, 2, 1) for q in range(len(want_tiles)) if mb[q] == c]
+    for runs, rpi in ((L["runs_gu"], L["rpi_gu"]), (L["runs_dn"], L["rpi_dn"])):
+        want_runs = [(q << 12) | j for q in order for j in range(rpi)]
+        assert runs.tolist() == want_runs
+
+
+@pytest.mark.parametrize("E,k,T", [(128, 8, 37), (128, 8, 512), (128, 8, 2048), (128, 8, 2050), (48, 8, 300),
+                                   (48, 8, 2048), (256, 16, 512), (256, 16, 1000), (64, 6, 101)])
+def test_grouped_bucketing_lists(hip_ready, E, k, T):
+    """The lists the grouped path builds on the device (the routing's 4-token
+    expert bitmaps, then the placement workgroups; past one chunk, chunk by
+    chunk) are the oracle's, bit for bit, on the layer's own routing."""
+    spec = W.LayerSpec(n_embd=1024, n_ff=256, n_expert=E)
+    case = Case(spec, seed=700 + E + k)
+    x = W.fill(W.NORMAL, 17, T, T * spec.n_embd, 0.0, 1.0).reshape(T, spec.n_embd)
+    print(f"  grouped lists E={E} k={k} T={T}", flush=True)
+    got, gi, gs, _ = case.gpu_batch(x, n_used=k, prefill_min=1)
+    L = ds3.grouped_lists()
+    print(f"    chunk {L['t0']}+{L['tc']}, from bitmaps: {L['marked']}, {len(L['tiles'])} work items", flush=True)
+    assert L["marked"]                            # the product path's placement, not the fallback
+    assert L["t0"] + L["tc"] == T
+    check_lists(L, gi, gs)
+    want, oi, osc, probs = case.oracle(x, n_used=k)
+    assert index_mismatches(gi, oi, probs) == 0
+    assert_close(got, want)
+
+
+def test_grouped_bucketing_lists_fallback(hip_ready):
+    """Router mode 2 routes the grouped path with the certified router, which
+    writes no bitmaps: the lists then come from the routed indices (k_bucket),
+    and are the same."""
+    spec = W.LayerSpec(n_embd=1024, n_ff=256, n_expert=128)
+    case = Case(spec, seed=712)
+    T = 300
+    x = W.fill(W.NORMAL, 18, T, T * spec.n_embd, 0.0, 1.0).reshape(T, spec.n_embd)
+    with router_mode(ds3.ROUTER_CERTIFIED):
+        _, gi, gs, _ = case.gpu_batch(x, prefill_min=1)
+    L = ds3.grouped_lists()
+    assert not L["marked"] and L["tc"] == T
+    check_lists(L, gi, gs)
+
+
+@pytest.mark.parametrize("T", [64, 512])
+def test_certified_router_grouped_weights(hip_ready, real, T):
+    """Router mode 2 on the grouped path: indices the reference's, and the
+    routing weights from the exact logits of the selected experts (a launch of
+    their sequential chains), so within the device expf / division of the
+    oracle's -- not the fp32 rounding of the certified sums."""
+    x = W.make_inputs(2, T, seed=117 + T)
+    want, oi, osc, probs = real.oracle(x)
+    with router_mode(ds3.ROUTER_CERTIFIED):
+        got, gi, gs, gl = real.gpu_batch(x, prefill_min=1)
+    assert index_mismatches(gi, oi, probs) == 0
+    same = (gi == oi).all(axis=1)
+    rel = np.abs(gs[same].astype(np.float64) - osc[same]) / osc[same]
+    print(f"    weights: max rel err {rel.max():.2e} over {int(same.sum())} rows", flush=True)
+    assert rel.max() <= 2e-6
+    ol = np.stack([O.vec_matmul(x[t], real.wr) for t in range(T)])
+    sel = np.take_along_axis(gl, gi, 1).view(np.uint32)
+    assert np.array_equal(sel[same], np.take_along_axis(ol, gi, 1).view(np.uint32)[same])   # exact logits
+    assert_close(got, want)
+
+
 # ---------------------------------------------------------------------------
 # full FFN, device-routed
 # ---------------------------------------------------------------------------
@@ -774,6 +860,70 @@ def test_invalid_arguments_return_error(hip_ready, real):
     assert hip().ds3_hip_matmul_quantized_batch(x, e.gate, out, 1, 4, 100, 144, 0, 12) == -1
     assert hip().ds3_hip_buffer_zero_f32(out, 6) == -1
     assert hip().ds3_hip_dequantize(x, 0, 12, 100, out) == -1
+
+
+def test_short_weight_buffers_return_error(hip_ready, real):
+    """Every MoE entry point refuses weights that do not hold what the call
+    would read on the device -- a router of fewer than n_expert rows, expert
+    tensors of fewer than n_expert experts, row strides shorter than a row, an
+    offset table of fewer than n_expert x 3 entries -- with -1 and the output
+    untouched, rather than reading past the buffer."""
+    d, e = real.dev, real.dev.experts
+    gs, us, dsd = e.strides
+    E, K, F = 128, 2048, 768
+    router = d.router
+    short_router = router.view(0, (E - 1) * K * 4)
+    short_gate = e.gate.view(0, (E - 1) * F * gs)
+    short_down = e.down.view(0, E * K * dsd - 1)
+    short_table = ds3.Buffer.alloc(E * 3 * 8 - 8)
+    full_table = ds3.Buffer.from_array(
+        np.array([[i * F * gs, i * F * us, i * K * dsd] for i in range(E)], np.uint64))
+    for T in (1, 64):
+        x = ds3.Buffer.from_array(W.make_inputs(2, T, seed=115))
+        out = ds3.Buffer.from_array(np.full(T * K, 7.0, np.float32))
+
+        def batch(fn, rt=router, g=e.gate, dn=e.down, gst=gs, table=None, rstride=K * 4):
+            return fn(x, rt, g, e.up, dn, 12, 12, 14, gst, us, dsd, table, out, None, None, None, None,
+                      T, K, E, 8, F, rstride, 0, True)
+
+        def block(rt=router, g=e.gate, dn=e.down, gst=gs, table=None, rstride=K * 4):
+            gain = ds3.Buffer.from_array(np.ones(K, np.float32))
+            return hip_fn("ds3_hip_moe_block")(out, gain, 1e-6, rt, g, e.up, dn, 12, 12, 14, gst, us, dsd, table,
+                                               None, None, None, None, T, K, E, 8, F, rstride, 0, True)
+
+        for fn in (hip_fn("ds3_hip_moe_ffn_batch"), hip_fn("ds3_hip_moe_ffn_batch_noalloc")):
+            print(f"  T={T} {fn.__name__}", flush=True)
+            assert batch(fn, rt=short_router) == -1
+            assert batch(fn, g=short_gate) == -1
+            assert batch(fn, dn=short_down) == -1
+            assert batch(fn, gst=gs - 1) == -1
+            assert batch(fn, rstride=K * 4 - 4) == -1
+            assert batch(fn, table=short_table) == -1
+        assert block(rt=short_router) == -1
+        assert block(g=short_gate) == -1
+        assert block(table=short_table) == -1
+        assert np.all(out.read(np.float32, T * K) == 7.0)
+        # a full table and full-size weights go through
+        assert batch(hip_fn("ds3_hip_moe_ffn_batch"), table=full_table) == 0
+    x1 = ds3.Buffer.from_array(W.make_inputs(1, 1, seed=116))
+    out1 = ds3.Buffer.from_array(np.full(K, 7.0, np.float32))
+    lg = ds3.Buffer.alloc(E * 4)
+    scr = ds3.Buffer.alloc(4096)
+
+    def moe_ffn(rt=router, g=e.gate, dn=e.down, table=None):
+        return hip_fn("ds3_hip_moe_ffn")(x1, rt, g, e.up, dn, 12, 12, 14, gs, us, dsd, None, None, None, 0, 0, 0,
+                                         0, 0, 0, out1, lg, table, scr, scr, scr, K, E, 8, F, 0, K * 4, 0, True)
+    assert moe_ffn(rt=short_router) == -1
+    assert moe_ffn(g=short_gate) == -1
+    assert moe_ffn(dn=short_down) == -1
+    assert moe_ffn(table=short_table) == -1
+    assert np.all(out1.read(np.float32, K) == 7.0)
+    assert moe_ffn() == 0
+
+
+def hip_fn(name):
+    from qw3_amd._native import hip
+    return getattr(hip(), name)
 
 
 # ---------------------------------------------------------------------------
