@@ -64,6 +64,9 @@ def parse():
     p.add_argument("--stack-block", action="store_true",
                    help="config 4: run each layer as the engine's FFN block (RMSNorm + MoE + residual)")
     p.add_argument("--t1-steps", type=int, default=208)
+    p.add_argument("--t1-zero", action="store_true",
+                   help="T=1 leg: zero the output before every call (default: each call accumulates into the "
+                        "output, the decode residual stream, with no zeroing launch)")
     p.add_argument("--no-t1", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
     p.add_argument("--skip", type=str, default="", help="default run: comma-separated legs to leave out (c3,c4,c5)")
@@ -204,8 +207,11 @@ def time_steps(step, steps, warmup, spec, T, n_used, first, per_kernel=True, gra
     return wall_ms, gpu_ms, stats, brk, counts
 
 
-def layer_steps(T, layers, xs, spec, n_used=8, noalloc=False):
-    """(step, first) for one layer call per step on T tokens, layers cycled."""
+def layer_steps(T, layers, xs, spec, n_used=8, noalloc=False, zero=True):
+    """(step, first) for one layer call per step on T tokens, layers cycled.
+    zero: the step first zeroes the output, as the engine's gathered prefill
+    does (reference src/ds3_engine.c:902); otherwise every call accumulates
+    into it, as a decode step adds the layer's output to the residual stream."""
     from qw3_amd import ds3
     E, K = spec.n_expert, spec.n_embd
     out = ds3.Buffer.alloc(T * K * 4)
@@ -213,7 +219,8 @@ def layer_steps(T, layers, xs, spec, n_used=8, noalloc=False):
 
     def step(i, want_idx=False):
         d = layers[i % len(layers)]
-        out.zero()
+        if zero:
+            out.zero()
         ds3.moe_ffn_batch(xs[i % len(xs)], d.router, spec.router_type, d.experts, out, T, E, n_used,
                           indices=idx if want_idx else None)
 
@@ -356,10 +363,11 @@ def make_layers(spec, n, what):
     return hosts[0], layers
 
 
-def leg_layer(args, config, T, steps, warmup, spec, layers, xs, traffic, n_used=8, what="", graph_of=0):
+def leg_layer(args, config, T, steps, warmup, spec, layers, xs, traffic, n_used=8, what="", graph_of=0,
+              zero=True):
     """One layer call per step on T tokens: figures, dominant-kernel roofline."""
     from qw3_amd import workload as W
-    step, first = layer_steps(T, layers, xs, spec, n_used)
+    step, first = layer_steps(T, layers, xs, spec, n_used, zero=zero)
     wall_ms, gpu_ms, stats, brk, counts = time_steps(step, steps, warmup, spec, T, n_used, first,
                                                      graph_of=graph_of)
     ms = wall_ms / steps
@@ -698,8 +706,10 @@ def main():
         # (--no-graph: each step enqueued from Python)
         g = 0 if args.no_graph else 16
         t1_steps = args.t1_steps if not g else max(g, args.t1_steps // g * g)
-        t1 = leg_layer(args, 1, 1, t1_steps, args.warmup, spec1, layers1, x1, traffic, what="t1", graph_of=g)
+        t1 = leg_layer(args, 1, 1, t1_steps, args.warmup, spec1, layers1, x1, traffic, what="t1", graph_of=g,
+                       zero=args.t1_zero)
         t1["graph"] = bool(g)
+        t1["output_zeroed_per_step"] = bool(args.t1_zero)
         for k in ("mfma_util", "expert_histogram", "tokens"):
             t1.pop(k, None)
         if not args.no_cpu:

@@ -27,7 +27,7 @@ constexpr int N_XCD_DEC = 8;   // MI355X: workgroups go round-robin to 8 XCDs
 #define DS3_DOWN_LDS 1         // Q6_K down rows staged through LDS by DMA
 #endif
 #ifndef DS3_SEL_RPW
-#define DS3_SEL_RPW 2          // rows per lane group in the fused-selection gate/up kernel
+#define DS3_SEL_RPW 4          // rows per lane group in the fused-selection gate/up kernel
 #endif
 
 // PAIR: h = swiglu(gate, up).  !PAIR: h = gate projection only, with expert
@@ -182,10 +182,22 @@ k_decode_gate_up_sel(const float *__restrict__ x, int n_used, ExpertWeights ew, 
     }
     const int r = blockIdx.x - ra.T, slot = r / nx, rb = r - slot * nx;
     const int t = slot / n_used, kk = slot - t * n_used;
-    const bool ok = cert_select_wave(cs.ca, ra, t, false, lane, e_rank);
+    // One wave ranks the token and hands the ranking to the others through
+    // LDS (the selection is a few hundred VALU instructions: repeated by
+    // every wave it cost more issue time than the rows' dot products).  The
+    // selecting wave rotates with the workgroup, so the selections of a CU's
+    // workgroups fall on different SIMDs.
+    __shared__ int sel_s[1 + WAVE];                           // certified flag, then the experts by rank
+    if (wave == (int)(blockIdx.x & (DEC_TPB / WAVE - 1))) {
+        const bool ok = cert_select_wave(cs.ca, ra, t, false, lane, e_rank);
+        if (lane == 0) sel_s[0] = ok ? 1 : 0;
+        if (ok && lane < n_used) sel_s[1 + lane] = e_rank;
+    }
     const bool emit = rb == 0 && kk == 0;
-    const bool certified = !__syncthreads_or(ok ? 0 : 1);   // pooled: the general path needs every wave
-    const int e = certified ? __builtin_amdgcn_readlane(e_rank, kk)
+    __syncthreads();
+    const bool certified = sel_s[0] != 0;                     // uniform: the general path needs every wave
+    if (certified) e_rank = lane < n_used ? sel_s[1 + lane] : 0;
+    const int e = certified ? sel_s[1 + kk]
                             : cert_select_tokens<1>(x, K, cs.w, cs.wstride, cs.ca, ra, t, emit, sel_prod)[kk];
     const uint32_t pf = certified ? prefetch_down_rows(ew, K, n_used, e_rank, lin, nwg) : 0u;
     gate_up_rows<GT, G, UPL, true, DS3_SEL_RPW>(x + (int64_t)t * K, slot, rb, e, ew, K, F, 0, h);
