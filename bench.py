@@ -15,6 +15,8 @@ puts each under its own key of the same line:
   c4  configs[3]  one token per step through 48 resident layers (HIP graph)
   c5  configs[4]  all-Q8_0 layer, T in {1, 4, 16, 64, 256, 1024}, on the GEMV
                   path and the grouped-MFMA path, with the crossover
+  dense           the engine's dense products beside the MoE: the output head
+                  GEMV (Q6_K, Q8_0) and a 512-row prefill projection (Q4_K)
 
 roofline: the dominant kernel's algorithmic bytes per launch / its mean
 duration, timed with HIP events on the library stream over a second pass of
@@ -69,7 +71,8 @@ def parse():
                         "output, the decode residual stream, with no zeroing launch)")
     p.add_argument("--no-t1", action="store_true")
     p.add_argument("--no-cpu", action="store_true")
-    p.add_argument("--skip", type=str, default="", help="default run: comma-separated legs to leave out (c3,c4,c5)")
+    p.add_argument("--skip", type=str, default="",
+                   help="default run: comma-separated legs to leave out (c3,c4,c5,dense)")
     p.add_argument("--cpu-tokens", type=int, default=512)
     p.add_argument("--copy-mib", type=int, default=0,
                    help="first run a plain device copy of this many MiB (k_copy, three times): the known-size "
@@ -458,6 +461,100 @@ def leg_c5(args, traffic):
     return r
 
 
+def leg_dense(args):
+    """The engine's dense quantised products beside the MoE (reference
+    src/ds3_engine.c:181-271): the output head (2048 -> 151,936 logits, one
+    token: vec_matmul, HBM-bound) in Q6_K and Q8_0, and a prefill projection
+    (M = 512 rows, 2048 -> 4096, Q4_K: matmul_quantized_batch) on its fp16
+    MFMA path and on its fp32 path.  Two weight copies alternate per call so
+    the head's 255-330 MB cannot stay in the 256 MB Infinity Cache."""
+    from qw3_amd import ds3
+    from qw3_amd import workload as W
+    from qw3_amd._native import hip
+    K, NH = 2048, 151936
+    out = {"workload": "output head 2048 -> 151,936 (one token) in Q6_K and Q8_0; prefill projection "
+                       "512 x 2048 -> 4096 in Q4_K; weights N(0, 0.02) quantised, x ~ N(0, 1)"}
+    rng = np.random.default_rng(5)
+    x = ds3.Buffer.from_array(rng.standard_normal(K).astype(np.float32))
+    y = ds3.Buffer.alloc(NH * 4)
+
+    def timed(name, call, n):
+        hip().ds3_hip_kernel_timing_reset()
+        hip().ds3_hip_kernel_timing_only(name.encode())
+        hip().ds3_hip_kernel_timing(1)
+        hip().ds3_hip_begin_batch()
+        t0 = time.perf_counter()
+        for i in range(n):
+            call(i)
+        hip().ds3_hip_end_batch()
+        wall = (time.perf_counter() - t0) / n
+        hip().ds3_hip_kernel_timing(0)
+        hip().ds3_hip_kernel_timing_only(None)
+        cnt, ms = ds3.kernel_stats()[name]
+        return ms / cnt / 1e3, wall
+
+    head = {}
+    for t in (ds3.TYPE_Q6_K, ds3.TYPE_Q8_0):
+        raw = W.quant_matrix(t, W.NORMAL, 7, t, NH, K, 0.0, 0.02)
+        ws = [ds3.Buffer.from_array(raw) for _ in range(2)]
+        rs = ds3.row_bytes(t, K)
+        call = lambda i: hip().ds3_hip_vec_matmul_quantized(x, ws[i % 2], y, K, NH, rs, t)
+        for i in range(4):
+            call(i)
+        k_s, wall = timed("gemv", call, 40)
+        b = NH * rs + K * 4 + NH * 4
+        head[ds3.TYPE_NAMES[t]] = {
+            "us_per_call": round(k_s * 1e6, 2), "wall_us_per_call": round(wall * 1e6, 2), "alg_bytes": b,
+            "roofline": {"bound": "hbm", "achieved": round(b / k_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(b / k_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "gemv"}}
+        log(f"[bench] dense: head {ds3.TYPE_NAMES[t]} {k_s * 1e6:.1f} us ({b / k_s / 1e12:.2f} TB/s)")
+        if t == ds3.TYPE_Q6_K and not args.no_cpu:
+            sys.path.insert(0, str(ROOT / "tests"))
+            import _oracle as O
+            Wf = (O.ref_dequantize if O.ref() is not None else O.dequantize)(t, raw, NH * K)
+            xh = np.ascontiguousarray(rng.standard_normal(K).astype(np.float32))
+            yh = np.empty(NH, np.float32)
+            fn = O.ref().ds3_ref_vec_matmul if O.ref() is not None else O.orc().orc_vec_matmul
+
+            def one():
+                t1 = time.perf_counter()
+                for _ in range(3):
+                    fn(O.ptr(xh), O.ptr(Wf), O.ptr(yh), K, NH)
+                return (time.perf_counter() - t1) / 3
+            dt, core = pinned_one_core(one)
+            head["Q6_K"]["cpu_baseline"] = {
+                "value": round(1.0 / dt, 3), "unit": "calls/s", "cores": 1,
+                "kind": "reference" if O.ref() is not None else "port", "pinned_cpu": core,
+                "sample": f"3 calls of ds3_ref_vec_matmul 2048 -> 151,936 on FP32-dequantised weights, one pinned "
+                          f"thread ({dt * 1e3:.0f} ms per call)", **host_cores()}
+            del Wf
+        del ws
+    out["head"] = head
+    M, N = 512, 4096
+    t = ds3.TYPE_Q4_K
+    raw = W.quant_matrix(t, W.NORMAL, 8, t, N, K, 0.0, 0.02)
+    wb = ds3.Buffer.from_array(raw)
+    A = ds3.Buffer.from_array(rng.standard_normal((M, K)).astype(np.float32))
+    C = ds3.Buffer.alloc(M * N * 4)
+    rs = ds3.row_bytes(t, K)
+    flops = 2 * M * N * K
+    proj = {"rows": M, "N": N, "K": K, "type": "Q4_K", "alg_flops": flops}
+    for name, min_rows in (("dense_mfma", 1), ("gemv", 1 << 30)):
+        prev = hip().ds3_hip_set_dense_mfma_min_rows(min_rows)
+        call = lambda i: hip().ds3_hip_matmul_quantized_batch(A, wb, C, M, N, K, rs, 0, t)
+        call(0)
+        k_s, wall = timed(name, call, 10)
+        hip().ds3_hip_set_dense_mfma_min_rows(prev)
+        key = "mfma_fp16" if name == "dense_mfma" else "fp32"
+        proj[key] = {"us_per_call": round(k_s * 1e6, 2), "wall_us_per_call": round(wall * 1e6, 2),
+                     "tflops": round(flops / k_s / 1e12, 2)}
+        log(f"[bench] dense: projection {M}x{K}->{N} Q4_K {key}: {k_s * 1e6:.1f} us ({flops / k_s / 1e12:.1f} TFLOP/s)")
+    proj["mfma_roofline"] = {"bound": "mfma", "achieved": proj["mfma_fp16"]["tflops"], "peak": FP16_PEAK_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(proj["mfma_fp16"]["tflops"] / FP16_PEAK_TFLOPS, 4)}
+    out["projection"] = proj
+    return out
+
+
 def leg_stack(args, traffic, n_used=8):
     """one token per step through a resident stack of
     --stack-layers MoE layers, h <- h + MoE_l(h) in place (the call
@@ -736,6 +833,8 @@ def main():
             line["c5"] = leg_c5(args, traffic)
         if "c4" not in skip:
             line["c4"] = leg_stack(args, traffic)
+        if "dense" not in skip:
+            line["dense"] = leg_dense(args)
     print(json.dumps(line), flush=True)
 
 

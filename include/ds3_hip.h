@@ -93,8 +93,20 @@ int ds3_hip_vec_matmul_q4k_simd(const ds3_hip_buffer_t *x, const ds3_hip_buffer_
 int ds3_hip_vec_matmul_q6k_simd(const ds3_hip_buffer_t *x, const ds3_hip_buffer_t *W, ds3_hip_buffer_t *y,
                                 uint32_t in_dim, uint32_t out_dim, uint64_t row_stride);
 
+/* reference src/ds3_metal.h:142-146: Q4_K product with an fp16 input vector
+ * x[in_dim] (widened exactly to fp32), y[out_dim] fp32. */
+int ds3_hip_vec_matmul_q4k_half(const ds3_hip_buffer_t *x, const ds3_hip_buffer_t *W, ds3_hip_buffer_t *y,
+                                uint32_t in_dim, uint32_t out_dim, uint64_t row_stride);
+
 /* reference src/ds3_metal.h:154-161: C[M][N] = A[M][K] . W[N][K]^T, fp32,
- * W at byte weight_offset inside the buffer. */
+ * W at byte weight_offset inside the buffer.  Below the dense-MFMA row
+ * count (ds3_hip_set_dense_mfma_min_rows, default 64) every product is an
+ * fp32 FMA on the exactly decoded weights, as the reference's kernel
+ * computes.  From that many rows, for Q4_K / Q6_K / Q8_0 with K a multiple of
+ * 512 and N a multiple of 256 (the engine's prefill projections), the
+ * product runs on the matrix cores with fp16 operands (A and the decoded
+ * weights rounded to fp16, fp32 accumulation), the precision of the MoE
+ * grouped products: relative L2 error ~5e-4 against fp32. */
 int ds3_hip_matmul_quantized_batch(const ds3_hip_buffer_t *A, const ds3_hip_buffer_t *W, ds3_hip_buffer_t *C,
                                    uint32_t M, uint32_t N, uint32_t K, uint64_t weight_row_stride,
                                    uint64_t weight_offset, ds3_hip_type_t type);
@@ -316,6 +328,11 @@ int ds3_hip_router_stats(uint64_t *certified, uint64_t *repaired, int reset);
 #define DS3_HIP_LISTS_META 12
 int ds3_hip_debug_grouped_lists(int32_t *meta, int32_t *counts, int32_t *offsets, int32_t *ids, float *wts,
                                 int32_t *slot_pos, int32_t *tiles, int32_t *runs_gu, int32_t *runs_dn);
+
+/* No ds3_metal.h counterpart: the row count of A from which
+ * ds3_hip_matmul_quantized_batch takes its fp16 MFMA path (see there).  0
+ * restores the default (64).  Returns the previous value. */
+int ds3_hip_set_dense_mfma_min_rows(int min_rows);
 
 /* ds3_hip_moe_ffn_batch uses the grouped (prefill) path when
  * n_tokens >= min_tokens, the per-token GEMV path otherwise.  0 restores the

@@ -29,6 +29,7 @@ typedef ds3_hip_buffer_t ds3_metal_buffer_t;
 #define ds3_metal_vec_matmul_q8_0_simd ds3_hip_vec_matmul_q8_0_simd
 #define ds3_metal_vec_matmul_q4k_simd ds3_hip_vec_matmul_q4k_simd
 #define ds3_metal_vec_matmul_q6k_simd ds3_hip_vec_matmul_q6k_simd
+#define ds3_metal_vec_matmul_q4k_half ds3_hip_vec_matmul_q4k_half
 #define ds3_metal_matmul_quantized_batch ds3_hip_matmul_quantized_batch
 #define ds3_metal_buffer_copy_f32 ds3_hip_buffer_copy_f32
 #define ds3_metal_buffer_zero_f32 ds3_hip_buffer_zero_f32

@@ -34,6 +34,7 @@ SIGNATURES: dict[str, tuple] = {
     "ds3_hip_vec_matmul_q8_0_simd": (C.c_int, [P, P, P, U32, U32, U64]),
     "ds3_hip_vec_matmul_q4k_simd": (C.c_int, [P, P, P, U32, U32, U64]),
     "ds3_hip_vec_matmul_q6k_simd": (C.c_int, [P, P, P, U32, U32, U64]),
+    "ds3_hip_vec_matmul_q4k_half": (C.c_int, [P, P, P, U32, U32, U64]),
     "ds3_hip_matmul_quantized_batch": (C.c_int, [P, P, P, U32, U32, U32, U64, U64, I32]),
     "ds3_hip_buffer_copy_f32": (C.c_int, [P, P, SZ]),
     "ds3_hip_buffer_zero_f32": (C.c_int, [P, SZ]),
@@ -75,6 +76,7 @@ SIGNATURES: dict[str, tuple] = {
     "ds3_hip_set_router_mode": (C.c_int, [C.c_int]),
     "ds3_hip_router_stats": (C.c_int, [C.POINTER(U64), C.POINTER(U64), C.c_int]),
     "ds3_hip_debug_grouped_lists": (C.c_int, [P, P, P, P, P, P, P, P, P]),
+    "ds3_hip_set_dense_mfma_min_rows": (C.c_int, [C.c_int]),
     "ds3_hip_set_prefill_min_tokens": (C.c_int, [C.c_int]),
     "ds3_hip_kernel_timing": (None, [C.c_int]),
     "ds3_hip_kernel_timing_reset": (None, []),

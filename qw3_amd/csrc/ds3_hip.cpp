@@ -40,6 +40,7 @@ static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 namespace {
 
 constexpr int kDefaultPrefillMin = 16;
+constexpr int kDefaultDenseMfmaMin = 64;   // matmul_quantized_batch: fp16 MFMA path from this many rows of A
 constexpr int kTickets = 32;             // router token-group tickets (zero between launches)
 constexpr int kCertMaxTokens = 16;       // automatic mode: certified router up to this many tokens
 #ifndef DS3_FUSE_SELECT_MAX_T
@@ -75,6 +76,7 @@ struct State {
     unsigned long long *cert_stats = nullptr;   // device {certified, repaired} token counts
     float *one_f = nullptr;          // device {1.0f}
     int prefill_min = kDefaultPrefillMin;
+    int dense_mfma_min = kDefaultDenseMfmaMin;
     // reference-style profiling (src/ds3_metal.m:2868-2885)
     bool profile = false;
     int cb_count = 0;
@@ -587,6 +589,39 @@ extern "C" int ds3_hip_vec_matmul_quantized(const ds3_hip_buffer_t *x, const ds3
     return vec_matmul_typed(x, W, y, in_dim, out_dim, row_stride, type, "vec_matmul_quantized");
 }
 
+// reference src/ds3_metal.h:142-146 (metal matmul_vec_q4k_half): x holds
+// fp16 values; they are widened exactly to fp32 and the Q4_K product runs as
+// for an fp32 x.
+extern "C" int ds3_hip_vec_matmul_q4k_half(const ds3_hip_buffer_t *x, const ds3_hip_buffer_t *W, ds3_hip_buffer_t *y,
+                                           uint32_t in_dim, uint32_t out_dim, uint64_t row_stride)
+{
+    if (!x || !W || !y || in_dim == 0 || !ensure_init()) return -1;
+    if (in_dim % 256 != 0) {
+        fprintf(stderr, "ds3_hip: vec_matmul_q4k_half in_dim=%u must be a multiple of 256\n", in_dim);
+        return -1;
+    }
+    if (!fits(x, (size_t)in_dim * 2, "x (fp16)")) return -1;
+    if (row_stride < row_bytes(T_Q4_K, in_dim)) {
+        fprintf(stderr, "ds3_hip: vec_matmul_q4k_half row_stride=%llu < one row\n", (unsigned long long)row_stride);
+        return -1;
+    }
+    if (!fits(y, (size_t)out_dim * 4, "y") || !fits(W, span_bytes(out_dim, row_stride, row_bytes(T_Q4_K, in_dim)), "W"))
+        return -1;
+    uint8_t *ws = ws_get((size_t)in_dim * 4);
+    if (!ws) return -1;
+    hipError_t e;
+    {
+        KScope ks("to_f32");
+        e = launch_to_f32((const _Float16 *)dptr(x), (float *)ws, in_dim, g.stream);
+    }
+    if (e == hipSuccess) {
+        KScope ks("gemv");
+        e = launch_gemv(T_Q4_K, (const float *)ws, in_dim, cptr(W), row_stride, fptr(y), out_dim, 1, (int)out_dim,
+                        (int)in_dim, nullptr, g.stream);
+    }
+    return finish(e, "vec_matmul_q4k_half");
+}
+
 extern "C" int ds3_hip_vec_matmul_f32_simd(const ds3_hip_buffer_t *x, const ds3_hip_buffer_t *W, ds3_hip_buffer_t *y,
                                            uint32_t in_dim, uint32_t out_dim, uint64_t row_stride)
 {
@@ -636,6 +671,40 @@ extern "C" int ds3_hip_matmul_quantized_batch(const ds3_hip_buffer_t *A, const d
     if (!fits(A, (size_t)M * K * 4, "A") || !fits(C, (size_t)M * N * 4, "C") ||
         !fits(W, weight_offset + (size_t)N * weight_row_stride, "W"))
         return -1;
+    if (weight_row_stride < row_bytes(type, K)) {
+        fprintf(stderr, "ds3_hip: matmul_quantized_batch weight_row_stride=%llu < one row\n",
+                (unsigned long long)weight_row_stride);
+        return -1;
+    }
+    if ((int64_t)M >= g.dense_mfma_min && dense_mfma_shape_ok(type, (int)N, (int)K) && M <= 65535) {
+        // fp16 MFMA path: A in fp16, the weights decoded to fp16, fp32
+        // accumulate, on the grouped gate_up kernel as one expert that holds
+        // every row of A (the bucketing lists of M zero expert indices)
+        const int rpi_gu = dense_runs_per_tile((int)N), rpi_dn = 1;   // down's list is written, not used
+        const int max_tiles = (int)((M + 63) / 64) + 1;
+        Bump bp;
+        const size_t o_x16 = bp.take((size_t)M * K * 2), o_idx = bp.take((size_t)M * 4), o_cnt = bp.take(16),
+                     o_off = bp.take(16), o_ids = bp.take((size_t)M * 4), o_wts = bp.take((size_t)M * 4),
+                     o_pos = bp.take((size_t)M * 4), o_tiles = bp.take((size_t)max_tiles * 4), o_nt = bp.take(16),
+                     o_rg = bp.take((size_t)max_tiles * rpi_gu * 4), o_rd = bp.take((size_t)max_tiles * rpi_dn * 4);
+        uint8_t *ws = ws_get(bp.off);
+        if (!ws) return -1;
+        BucketOut bo{ (int32_t *)(ws + o_cnt), (int32_t *)(ws + o_off), (int32_t *)(ws + o_ids), (float *)(ws + o_wts),
+                      (int32_t *)(ws + o_pos), (int32_t *)(ws + o_tiles), (int32_t *)(ws + o_nt), max_tiles, 64,
+                      (int32_t *)(ws + o_rg), (int32_t *)(ws + o_rd), (int32_t *)(ws + o_nt) + 1, rpi_gu, rpi_dn };
+        hipError_t e = launch_fill_zero((float *)(ws + o_idx), M, g.stream);      // expert 0 for every row
+        if (e == hipSuccess) e = launch_to_f16(fptr(A), (_Float16 *)(ws + o_x16), (int64_t)M * K, g.stream);
+        if (e == hipSuccess) {
+            KScope ks("dense_lists");
+            e = launch_bucket((const int32_t *)(ws + o_idx), (const float *)(ws + o_idx), (int)M, 1, 1, bo, g.stream);
+        }
+        if (e == hipSuccess) {
+            KScope ks("dense_mfma");
+            e = launch_dense_mfma((const _Float16 *)(ws + o_x16), (int)K, cptr(W) + weight_offset, weight_row_stride,
+                                  type, (int)N, bo, fptr(C), g.stream);
+        }
+        return finish(e, "matmul_quantized_batch");
+    }
     KScope ks("gemv");
     return finish(launch_gemv(type, fptr(A), K, cptr(W) + weight_offset, weight_row_stride, fptr(C), N, (int)M,
                               (int)N, (int)K, nullptr, g.stream),
@@ -1557,6 +1626,13 @@ extern "C" int ds3_hip_set_router_mode(int mode)
 {
     const int prev = g.router_mode;
     g.router_mode = (mode >= 0 && mode <= 2) ? mode : 0;
+    return prev;
+}
+
+extern "C" int ds3_hip_set_dense_mfma_min_rows(int min_rows)
+{
+    const int prev = g.dense_mfma_min;
+    g.dense_mfma_min = min_rows > 0 ? min_rows : kDefaultDenseMfmaMin;
     return prev;
 }
 

@@ -100,6 +100,13 @@ __global__ void k_to_f16(const float *x, _Float16 *y, int64_t n4)
     ((half4 *)y)[i] = h;
 }
 
+// fp16 -> fp32, exact; one element per thread (any n, 2-byte aligned input).
+__global__ void k_to_f32(const _Float16 *x, float *y, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * EW_TPB + threadIdx.x;
+    if (i < n) y[i] = (float)x[i];
+}
+
 // out[t][j] = (acc ? out[t][j] : 0) + w_0 y[p_0][j] + ... in k order, then + residual.
 // Four consecutive columns per thread when N % 4 == 0 (VEC = 4), else one.
 template <int VEC>
@@ -235,6 +242,13 @@ hipError_t launch_to_f16(const float *x, _Float16 *y, int64_t n, hipStream_t s)
 {
     if (n % 4) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_to_f16, grid1d(n / 4), dim3(EW_TPB), 0, s, x, y, n / 4);
+    return hipGetLastError();
+}
+
+hipError_t launch_to_f32(const _Float16 *x, float *y, int64_t n, hipStream_t s)
+{
+    if (n <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_to_f32, grid1d(n), dim3(EW_TPB), 0, s, x, y, n);
     return hipGetLastError();
 }
 

@@ -178,6 +178,7 @@ hipError_t launch_bucket_place(const int32_t *idx, const float *scores, const ui
 
 // Prefill grouped products (fp16 MFMA, fp32 accumulate).
 hipError_t launch_to_f16(const float *x, _Float16 *y, int64_t n, hipStream_t s);
+hipError_t launch_to_f32(const _Float16 *x, float *y, int64_t n, hipStream_t s);
 hipError_t launch_grouped_gate_up(const _Float16 *x16, int K, const ExpertWeights &ew, int F,
                                   const BucketOut &b, _Float16 *h16, hipStream_t s);
 hipError_t launch_grouped_down(const _Float16 *h16, int F, const ExpertWeights &ew, int N,
@@ -191,6 +192,16 @@ bool grouped_shape_ok(int n_embd, int n_ff);
 // n-runs per token tile of the grouped kernels for a layer shape (BucketOut
 // rpi_gu / rpi_dn).
 void grouped_runs_per_tile(int n_embd, int n_ff, int &rpi_gu, int &rpi_dn);
+
+// Dense C[M][N] = A W^T (fp16 operands, fp32 accumulate) on the grouped
+// gate_up kernel: x16 = A [M][K] in fp16; b = the bucketing lists of one
+// expert holding rows 0 .. M-1 (launch_bucket of M zero indices, k = 1,
+// E = 1, dense_runs_per_tile(N) gate_up runs per token tile); W rows stride
+// bytes apart.  Shapes: dense_mfma_shape_ok.
+bool dense_mfma_shape_ok(int type, int N, int K);
+int dense_runs_per_tile(int N);
+hipError_t launch_dense_mfma(const _Float16 *x16, int K, const uint8_t *w, uint64_t stride, int type, int N,
+                             const BucketOut &b, float *c, hipStream_t s);
 
 // out[t][j] = (accumulate ? out : 0) + sum_k w[t][k] * y[slot_pos[t*k+kk]][j] (+ residual)
 hipError_t launch_combine(const float *y, const int32_t *slot_pos, const float *wts, int T, int k,

@@ -36,6 +36,8 @@
 #include "common.h"
 #include "launch.h"
 
+#include <type_traits>
+
 namespace ds3k {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -667,6 +669,31 @@ struct GgEpiDown {
     }
 };
 
+// Plain-product epilogue (dense C = A W^T on the gate_up kernel): the two
+// row sets of a run are the two halves of W, rows n and n + half; C rows in
+// fp32 (each store instruction writes 4 rows x 16 consecutive columns).
+struct GgEpiPlain {
+    float *c;
+    int N, half, row0, mrows, nt0, wave, lane;
+    template <int MB>
+    __device__ __forceinline__ void store(const floatx4 (&acc)[MB][2], int t) const
+    {
+        const int g = lane >> 4, m = lane & 15;
+        const int col = (nt0 + t) * GG_TILE_N + 16 * wave + m;
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int mr = 16 * mb + 4 * g + j;
+                if (mr < mrows) {
+                    float *row = c + (int64_t)(row0 + mr) * N;
+                    row[col] = acc[mb][0][j];
+                    row[half + col] = acc[mb][1][j];
+                }
+            }
+    }
+};
+
 template <int TYPE, bool AL, int NB, int D, class Epi>
 __device__ __forceinline__ void gg_run_mb(int mb, const uint8_t *const (&rows)[NB], uint64_t tstride, int S, int nnt,
                                           uint32_t a_lds, uint32_t step_bytes, const uint32_t (&lofs)[8], int g,
@@ -712,11 +739,11 @@ struct GgAChunks {
     }
 };
 
-template <int TYPE, bool AL, int MB>
+template <int TYPE, bool AL, int MB, class Epi>
 __device__ __forceinline__ void gg_gate_up_run(const _Float16 *x16, int K, const int32_t *ids, int mrows,
                                                const uint8_t *const (&rows)[2], uint64_t tstride, int nnt,
                                                uint32_t a_lds, const uint32_t (&lofs)[8], int wave, int lane,
-                                               const GgEpiGateUp &epi)
+                                               const Epi &epi)
 {
     const int S = K / 256;
     GgAChunks<MB> as;
@@ -733,10 +760,12 @@ __device__ __forceinline__ void gg_gate_up_run(const _Float16 *x16, int K, const
                                                                    epi);
 }
 
-template <int TYPE>
+// PLAIN: a dense product C[M][2F] = A W^T instead (one expert, W's rows
+// [0, F) in the gate slot and [F, 2F) in the up slot), fp32 C in place of h.
+template <int TYPE, bool PLAIN = false>
 __global__ void __launch_bounds__(64 * GG_WV)
 k_grouped_gate_up(const _Float16 *__restrict__ x16, int K, ExpertWeights ew, int F, BucketOut b,
-                  _Float16 *__restrict__ h16, int ntb)
+                  _Float16 *__restrict__ h16, int ntb, float *__restrict__ c = nullptr)
 {
     __shared__ __attribute__((aligned(16))) uint8_t smem[GG_GU_LDS];
     const int n_nt = F / GG_TILE_N;
@@ -765,8 +794,11 @@ k_grouped_gate_up(const _Float16 *__restrict__ x16, int K, ExpertWeights ew, int
         const size_t r0 = (size_t)nt0 * GG_TILE_N + 16 * wave + (lane & 15);
         const uint8_t *const rows[2] = { wg + r0 * ew.gate_stride, wu + r0 * ew.up_stride };
         const uint64_t tstride = (uint64_t)GG_TILE_N * ew.gate_stride;    // gate and up strides are equal
-        const GgEpiGateUp epi{ h16, F, it.off + it.m0, mrows, nt0, wave, lane, stage };
         const bool al = gg_aligned<TYPE>(wg, wu, ew.gate_stride);
+        using Epi = std::conditional_t<PLAIN, GgEpiPlain, GgEpiGateUp>;
+        Epi epi;
+        if constexpr (PLAIN) epi = GgEpiPlain{ c, 2 * F, F, it.off + it.m0, mrows, nt0, wave, lane };
+        else epi = GgEpiGateUp{ h16, F, it.off + it.m0, mrows, nt0, wave, lane, stage };
 #define DS3_GU_CASE(MBV)                                                                                      \
     if (al) gg_gate_up_run<TYPE, true, MBV>(x16, K, ids, mrows, rows, tstride, nnt, a_lds, lofs, wave, lane, epi); \
     else gg_gate_up_run<TYPE, false, MBV>(x16, K, ids, mrows, rows, tstride, nnt, a_lds, lofs, wave, lane, epi);
@@ -824,6 +856,12 @@ k_grouped_down(const _Float16 *__restrict__ h16, int F, ExpertWeights ew, int N,
             gg_run_mb<TYPE, false, 1, DS3_GG_DEPTH>(mblocks, rows, tstride, S, nnt, a_lds, step_bytes, lofs, g, epi);
     }
 }
+
+// Dense C[M][N] = A[M][K] W[N][K]^T on the gate_up kernel: the bucketing
+// lists of one expert holding every row of A (b), x16 = A in fp16.
+template <int TV>
+static hipError_t dense_t(const _Float16 *x16, int K, const ExpertWeights &ew, int N, const BucketOut &b, float *c,
+                          hipStream_t s);
 
 bool grouped_type_ok(int type, int K)
 {
@@ -898,6 +936,48 @@ hipError_t launch_grouped_gate_up(const _Float16 *x16, int K, const ExpertWeight
     case T_Q4_K: return gate_up_t<T_Q4_K>(x16, K, ew, F, b, h16, s);
     case T_Q6_K: return gate_up_t<T_Q6_K>(x16, K, ew, F, b, h16, s);
     case T_Q8_0: return gate_up_t<T_Q8_0>(x16, K, ew, F, b, h16, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <int TV>
+static hipError_t dense_t(const _Float16 *x16, int K, const ExpertWeights &ew, int N, const BucketOut &b, float *c,
+                          hipStream_t s)
+{
+    // one n tile per run: a dense product has few token tiles, so the runs,
+    // not the tiles, must fill the CUs
+    const unsigned grid = gg_grid(b.max_tiles * b.rpi_gu);
+    hipLaunchKernelGGL((k_grouped_gate_up<TV, true>), dim3(grid), dim3(64 * GG_WV), 0, s, x16, K, ew, N / 2, b,
+                       nullptr, 1, c);
+    return hipGetLastError();
+}
+
+bool dense_mfma_shape_ok(int type, int N, int K)
+{
+    return grouped_type_ok(type, K) && K % (256 * DS3_GU_DEPTH) == 0 && N > 0 && N % (2 * GG_TILE_N) == 0;
+}
+
+int dense_runs_per_tile(int N) { return N / 2 / GG_TILE_N; }
+
+hipError_t launch_dense_mfma(const _Float16 *x16, int K, const uint8_t *w, uint64_t stride, int type, int N,
+                             const BucketOut &b, float *c, hipStream_t s)
+{
+    const int rg = dense_runs_per_tile(N);
+    const uint64_t row_b = type == T_Q8_0 ? (uint64_t)(K / 32) * 34 : (uint64_t)(K / 256) * (type == T_Q4_K ? 144 : 210);
+    if (!dense_mfma_shape_ok(type, N, K) || b.tile_m != GG_TILE_M || b.runs_gu == nullptr || b.rpi_gu != rg ||
+        stride < row_b)
+        return hipErrorInvalidValue;
+    ExpertWeights ew{};
+    ew.gate = w;
+    ew.up = w + (uint64_t)(N / 2) * stride;
+    ew.down = nullptr;
+    ew.gate_stride = ew.up_stride = stride;
+    ew.gate_type = ew.up_type = type;
+    ew.table = nullptr;
+    switch (type) {
+    case T_Q4_K: return dense_t<T_Q4_K>(x16, K, ew, N, b, c, s);
+    case T_Q6_K: return dense_t<T_Q6_K>(x16, K, ew, N, b, c, s);
+    case T_Q8_0: return dense_t<T_Q8_0>(x16, K, ew, N, b, c, s);
     default: return hipErrorInvalidValue;
     }
 }
