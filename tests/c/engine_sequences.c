@@ -18,12 +18,26 @@
  *           bucketing -> per expert gather_rows, matmul_quantized_batch
  *           x3, silu_mul, scatter_add_weighted -> vec_add(ffn_out, residual)
  *
+ * and the device-routed sequences that replace the host read-back and host
+ * bucketing on a discrete GPU (no ds3_metal.h counterpart for the last three):
+ *   gpu-only decode (reference src/ds3_engine.c:638-720): per token rms_norm
+ *           -> zero ffn_out -> moe_ffn (router, top-k and experts on the
+ *           device, expert offset table) -> vec_add(ffn_out, residual)
+ *   block   per token ds3_hip_moe_block: hidden += MoE(rms_norm(hidden) * g)
+ *           in place, the engine's whole FFN block in one call
+ *   graph   the same T block calls captured once as a HIP graph
+ *           (ds3_hip_graph_begin / _end) and replayed on the same input
+ *   batch   the prefill chunk in one ds3_hip_moe_ffn_batch call (routing,
+ *           bucketing, grouped products and combine on the device) into the
+ *           zeroed ffn_out, with the residual added by the call
+ *
  * Usage: engine_sequences <dir>, with <dir>/meta.txt holding
  *   E K F k T gate_type up_type down_type off_router off_gate off_up off_down
  *   blob_bytes
  * and <dir>/{weights.bin, hidden.f32, gain.f32, residual.f32}.  Writes
  * <dir>/{decode_out.f32, decode_idx.i32, prefill_out.f32, prefill_idx.i32,
- * norm.f32}.  Exit status 0 on success.
+ * norm.f32, gpuonly_out.f32, block_out.f32, block_idx.i32, graph_out.f32,
+ * batch_out.f32, batch_idx.i32}.  Exit status 0 on success.
  */
 #define _DEFAULT_SOURCE
 #include <fcntl.h>
@@ -247,6 +261,107 @@ int main(int argc, char **argv)
         for (size_t i = 0; i < sizeof bs / sizeof bs[0]; i++) ds3_metal_buffer_free(bs[i]);
     }
 
+    /* ------------------------------------------------ gpu-only decode (moe_ffn) */
+    {
+        /* the engine's [E][3] expert offset table (src/ds3_engine.c:1747-1773) */
+        uint64_t *tbl = malloc((size_t)E * 3 * sizeof(uint64_t));
+        CHECK(tbl != NULL);
+        for (unsigned e = 0; e < E; e++) {
+            tbl[3 * e + 0] = (uint64_t)e * F * gs;
+            tbl[3 * e + 1] = (uint64_t)e * F * us;
+            tbl[3 * e + 2] = (uint64_t)e * K * ds;
+        }
+        ds3_metal_buffer_t *b_tbl = ds3_metal_buffer_alloc((size_t)E * 3 * sizeof(uint64_t));
+        ds3_metal_buffer_t *b_hidden = ds3_metal_buffer_alloc((size_t)K * 4);
+        ds3_metal_buffer_t *b_norm = ds3_metal_buffer_alloc((size_t)K * 4);
+        ds3_metal_buffer_t *b_res = ds3_metal_buffer_alloc((size_t)K * 4);
+        ds3_metal_buffer_t *b_ffn = ds3_metal_buffer_alloc((size_t)K * 4);
+        ds3_metal_buffer_t *b_logits = ds3_metal_buffer_alloc((size_t)E * 4);
+        ds3_metal_buffer_t *b_mh = ds3_metal_buffer_alloc((size_t)k * F * 4);
+        ds3_metal_buffer_t *b_mu = ds3_metal_buffer_alloc((size_t)k * F * 4);
+        ds3_metal_buffer_t *b_md = ds3_metal_buffer_alloc((size_t)k * K * 4);
+        CHECK(b_tbl && b_hidden && b_norm && b_res && b_ffn && b_logits && b_mh && b_mu && b_md);
+        CHECK(ds3_metal_buffer_write(b_tbl, 0, tbl, (size_t)E * 3 * sizeof(uint64_t)) == 0);
+        for (unsigned t = 0; t < T; t++) {
+            CHECK(ds3_metal_buffer_write(b_hidden, 0, hidden + (size_t)t * K, (size_t)K * 4) == 0);
+            CHECK(ds3_metal_buffer_write(b_res, 0, residual + (size_t)t * K, (size_t)K * 4) == 0);
+            CHECK(ds3_metal_rms_norm(b_hidden, b_ffn_norm, b_norm, K, 1, NORM_EPS) == 0);
+            CHECK(ds3_metal_buffer_zero_f32(b_ffn, (size_t)K * 4) == 0);
+            CHECK(ds3_metal_moe_ffn(b_norm, router, gate, up, down, gt, ut, dt, gs, us, ds, NULL, NULL, NULL,
+                                    DS3_HIP_TYPE_F32, DS3_HIP_TYPE_F32, DS3_HIP_TYPE_F32, 0, 0, 0, b_ffn, b_logits,
+                                    b_tbl, b_mh, b_mu, b_md, K, E, k, F, 0, rs, DS3_HIP_TYPE_F32, true) == 0);
+            CHECK(ds3_metal_vec_add(b_ffn, b_res, b_hidden, K) == 0);
+            CHECK(ds3_metal_buffer_read(b_hidden, 0, out + (size_t)t * K, (size_t)K * 4) == 0);
+        }
+        CHECK(write_file(dir, "gpuonly_out.f32", out, (size_t)T * K * 4) == 0);
+        ds3_metal_buffer_t *bs[] = { b_tbl, b_hidden, b_norm, b_res, b_ffn, b_logits, b_mh, b_mu, b_md };
+        for (size_t i = 0; i < sizeof bs / sizeof bs[0]; i++) ds3_metal_buffer_free(bs[i]);
+        free(tbl);
+    }
+
+    /* --------------------------------------- block per token, then as one graph */
+    {
+        ds3_metal_buffer_t *b_hid = ds3_metal_buffer_alloc((size_t)T * K * 4);
+        ds3_metal_buffer_t *b_idx = ds3_metal_buffer_alloc((size_t)T * k * 4);
+        CHECK(b_hid && b_idx);
+        ds3_metal_buffer_t *hv[256], *iv[256];
+        CHECK(T <= 256);
+        for (unsigned t = 0; t < T; t++) {
+            hv[t] = ds3_metal_buffer_view(b_hid, (size_t)t * K * 4, (size_t)K * 4);
+            iv[t] = ds3_metal_buffer_view(b_idx, (size_t)t * k * 4, (size_t)k * 4);
+            CHECK(hv[t] && iv[t]);
+        }
+        CHECK(ds3_metal_buffer_write(b_hid, 0, hidden, (size_t)T * K * 4) == 0);
+        for (unsigned t = 0; t < T; t++)
+            CHECK(ds3_hip_moe_block(hv[t], b_ffn_norm, NORM_EPS, router, gate, up, down, gt, ut, dt, gs, us, ds, NULL,
+                                    NULL, NULL, iv[t], NULL, 1, K, E, k, F, rs, DS3_HIP_TYPE_F32, true) == 0);
+        CHECK(ds3_metal_buffer_read(b_hid, 0, out, (size_t)T * K * 4) == 0);
+        CHECK(ds3_metal_buffer_read(b_idx, 0, idx_all, (size_t)T * k * 4) == 0);
+        CHECK(write_file(dir, "block_out.f32", out, (size_t)T * K * 4) == 0);
+        CHECK(write_file(dir, "block_idx.i32", idx_all, (size_t)T * k * 4) == 0);
+        /* the same calls captured once and replayed on the same input */
+        void *graph = NULL;
+        CHECK(ds3_hip_graph_begin() == 0);
+        for (unsigned t = 0; t < T; t++)
+            CHECK(ds3_hip_moe_block(hv[t], b_ffn_norm, NORM_EPS, router, gate, up, down, gt, ut, dt, gs, us, ds, NULL,
+                                    NULL, NULL, iv[t], NULL, 1, K, E, k, F, rs, DS3_HIP_TYPE_F32, true) == 0);
+        CHECK(ds3_hip_graph_end(&graph) == 0 && graph != NULL);
+        CHECK(ds3_metal_buffer_write(b_hid, 0, hidden, (size_t)T * K * 4) == 0);
+        CHECK(ds3_hip_graph_launch(graph) == 0);
+        CHECK(ds3_metal_buffer_read(b_hid, 0, out, (size_t)T * K * 4) == 0);
+        CHECK(write_file(dir, "graph_out.f32", out, (size_t)T * K * 4) == 0);
+        ds3_hip_graph_destroy(graph);
+        for (unsigned t = 0; t < T; t++) {
+            ds3_metal_buffer_free(hv[t]);
+            ds3_metal_buffer_free(iv[t]);
+        }
+        ds3_metal_buffer_free(b_hid);
+        ds3_metal_buffer_free(b_idx);
+    }
+
+    /* ------------------------------------------- prefill chunk in one batch call */
+    {
+        const unsigned M = T;
+        ds3_metal_buffer_t *b_hidden = ds3_metal_buffer_alloc((size_t)M * K * 4);
+        ds3_metal_buffer_t *b_norm = ds3_metal_buffer_alloc((size_t)M * K * 4);
+        ds3_metal_buffer_t *b_res = ds3_metal_buffer_alloc((size_t)M * K * 4);
+        ds3_metal_buffer_t *b_ffn = ds3_metal_buffer_alloc((size_t)M * K * 4);
+        ds3_metal_buffer_t *b_idx = ds3_metal_buffer_alloc((size_t)M * k * 4);
+        CHECK(b_hidden && b_norm && b_res && b_ffn && b_idx);
+        CHECK(ds3_metal_buffer_write(b_hidden, 0, hidden, (size_t)M * K * 4) == 0);
+        CHECK(ds3_metal_buffer_write(b_res, 0, residual, (size_t)M * K * 4) == 0);
+        CHECK(ds3_metal_rms_norm(b_hidden, b_ffn_norm, b_norm, K, M, NORM_EPS) == 0);
+        CHECK(ds3_metal_buffer_zero_f32(b_ffn, (size_t)M * K * 4) == 0);
+        CHECK(ds3_hip_moe_ffn_batch(b_norm, router, gate, up, down, gt, ut, dt, gs, us, ds, NULL, b_ffn, b_res, NULL,
+                                    b_idx, NULL, M, K, E, k, F, rs, DS3_HIP_TYPE_F32, true) == 0);
+        CHECK(ds3_metal_buffer_read(b_ffn, 0, out, (size_t)M * K * 4) == 0);
+        CHECK(ds3_metal_buffer_read(b_idx, 0, idx_all, (size_t)M * k * 4) == 0);
+        CHECK(write_file(dir, "batch_out.f32", out, (size_t)M * K * 4) == 0);
+        CHECK(write_file(dir, "batch_idx.i32", idx_all, (size_t)M * k * 4) == 0);
+        ds3_metal_buffer_t *bs[] = { b_hidden, b_norm, b_res, b_ffn, b_idx };
+        for (size_t i = 0; i < sizeof bs / sizeof bs[0]; i++) ds3_metal_buffer_free(bs[i]);
+    }
+
     ds3_metal_buffer_free(router);
     ds3_metal_buffer_free(gate);
     ds3_metal_buffer_free(up);
@@ -262,6 +377,6 @@ int main(int argc, char **argv)
     free(norm_rows);
     free(idx_all);
     free(sc_all);
-    fprintf(stderr, "engine_sequences: decode and prefill done, T=%u E=%u\n", T, E);
+    fprintf(stderr, "engine_sequences: decode, prefill, gpu-only, block, graph and batch done, T=%u E=%u\n", T, E);
     return 0;
 }

@@ -75,7 +75,14 @@ def test_engine_call_sequences(hip_ready, tmp_path):
     vec_add) and its gathered prefill (per-token router, topk_batch_tokens,
     host bucketing, gather / matmul_quantized_batch x3 / silu_mul /
     scatter_add per expert, vec_add) on a Q4_K/Q6_K layer imported with
-    buffer_from_mmap; both match the oracle run on the same normalised rows."""
+    buffer_from_mmap, then the device-routed sequences that replace the
+    read-back and host bucketing: the GPU-only decode through moe_ffn with the
+    expert offset table (src/ds3_engine.c:638-720), moe_block per token, the
+    same block calls as one captured graph, and the prefill chunk through one
+    moe_ffn_batch call.  Every sequence matches the oracle on the same
+    normalised rows; the device-routed ones match the legacy sequence of
+    their kind (indices identical, MoE outputs within the bar), and the
+    graph replay equals the eager block calls bit for bit."""
     if not HARNESS.exists():
         pytest.skip("tests/c/_build/engine_sequences was not built")
     spec = W.LayerSpec(n_expert=32)
@@ -97,14 +104,35 @@ def test_engine_call_sequences(hip_ready, tmp_path):
     print(r.stderr[-1500:], flush=True)
     assert r.returncode == 0, r.stderr[-2000:]
     norm = np.fromfile(tmp_path / "norm.f32", np.float32).reshape(T, K)
-    want, oi, _, probs = case.oracle(norm)
-    want = want + residual
+    moe, oi, _, probs = case.oracle(norm)
+    want = moe + residual
+    load = lambda name, dt=np.float32, n=K: np.fromfile(tmp_path / name, dt).reshape(T, n)
+    legacy = {}
     for what in ("decode", "prefill"):
-        got = np.fromfile(tmp_path / f"{what}_out.f32", np.float32).reshape(T, K)
-        gi = np.fromfile(tmp_path / f"{what}_idx.i32", np.int32).reshape(T, k)
+        got = load(f"{what}_out.f32")
+        gi = load(f"{what}_idx.i32", np.int32, k)
         print(f"    {what}", flush=True)
         assert index_mismatches(gi, oi, probs) == 0
         assert_close(got, want)
+        legacy[what] = (got - residual, gi)
+    # the device-routed replacements of the read-back and host bucketing, on
+    # the same inputs: against the oracle, and their MoE parts and routing
+    # against the legacy sequence of the same kind (decode or prefill)
+    base = {"gpuonly": residual, "block": hidden, "graph": hidden, "batch": residual}
+    kind = {"gpuonly": "decode", "block": "decode", "graph": "decode", "batch": "prefill"}
+    for what, x0 in base.items():
+        got = load(f"{what}_out.f32")
+        print(f"    {what}", flush=True)
+        assert_close(got, moe + x0)
+        lmoe, lidx = legacy[kind[what]]
+        assert_close(got - x0, lmoe.astype(np.float64))
+        idx_file = tmp_path / f"{what}_idx.i32"
+        if idx_file.exists():
+            gi = load(f"{what}_idx.i32", np.int32, k)
+            assert index_mismatches(gi, oi, probs) == 0
+            assert np.array_equal(gi, lidx)
+    # the captured graph replays the eager block calls bit for bit
+    assert np.array_equal(load("graph_out.f32").view(np.uint32), load("block_out.f32").view(np.uint32))
 
 
 def test_gguf_residency_offset_table(hip_ready):
