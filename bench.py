@@ -42,7 +42,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
 FP16_PEAK_TFLOPS = 2500.0      # dense fp16 MFMA
-C5_TOKENS = (1, 4, 16, 64, 256, 1024)
+C5_TOKENS = (1, 4, 8, 16, 64, 256, 1024)
 
 
 def log(*a):
@@ -236,7 +236,8 @@ def layer_steps(T, layers, xs, spec, n_used=8, noalloc=False, zero=True):
 
 def roofline(stats, spec, T, counts, n_used, traffic):
     """traffic: {kernel: HBM bytes per launch} measured at T = 512, and at
-    T = 1 under "T1/<kernel>" (T = 2048 under "T2048/")."""
+    T = 1 under "T1/<kernel>" (T = 2048 under "T2048/"); the all-Q8_0 layer's
+    under "Q8_0/T<T>/"."""
     name = next(iter(stats))                  # the one kernel timed in the second pass
     n, ms = stats[name]
     avg_s = ms / n / 1e3
@@ -245,8 +246,13 @@ def roofline(stats, spec, T, counts, n_used, traffic):
     r = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
          "kernel_avg_us": round(avg_s * 1e6, 2), "alg_bytes_per_launch": b}
-    key = {1: "T1/", 512: "", 2048: "T2048/"}.get(T)
-    if traffic and key is not None and key + name in traffic and spec.gate_type == 12:
+    if spec.gate_type == 12:
+        key = {1: "T1/", 512: "", 2048: "T2048/"}.get(T)
+    elif spec.gate_type == 8:
+        key = f"Q8_0/T{T}/"
+    else:
+        key = None
+    if traffic and key is not None and key + name in traffic:
         r["traffic"] = traffic[key + name]
     return r
 

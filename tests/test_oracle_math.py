@@ -12,12 +12,17 @@ RNG = np.random.default_rng(7)
 
 
 def test_fp16_decode_exhaustive():
-    """Every binary16 pattern decodes to numpy's float16 value, bit for bit."""
+    """Every one of the 65,536 binary16 patterns decodes to numpy's float16
+    value, bit for bit: all of them through the oracle's F16 dequantisation
+    (one call), and every 97th also through its scalar orc_fp16_to_fp32."""
     h = np.arange(1 << 16, dtype=np.uint16)
-    got = np.array([O.orc().orc_fp16_to_fp32(int(v)) for v in h[::97]], np.float32)
-    want = h[::97].view(np.float16).astype(np.float32)
+    want = h.view(np.float16).astype(np.float32)
+    got = O.dequantize(ds3.TYPE_F16, h.view(np.uint8), h.size)
     same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
     assert same.all()
+    one = np.array([O.orc().orc_fp16_to_fp32(int(v)) for v in h[::97]], np.float32)
+    same1 = (one.view(np.uint32) == want[::97].view(np.uint32)) | (np.isnan(one) & np.isnan(want[::97]))
+    assert same1.all()
 
 
 def test_q8_0_exactly_representable_roundtrip():
