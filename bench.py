@@ -507,12 +507,12 @@ def leg_dense(args):
         call = lambda i: hip().ds3_hip_vec_matmul_quantized(x, ws[i % 2], y, K, NH, rs, t)
         for i in range(4):
             call(i)
-        k_s, wall = timed("gemv", call, 40)
+        k_s, wall = timed("gemv1", call, 40)
         b = NH * rs + K * 4 + NH * 4
         head[ds3.TYPE_NAMES[t]] = {
             "us_per_call": round(k_s * 1e6, 2), "wall_us_per_call": round(wall * 1e6, 2), "alg_bytes": b,
             "roofline": {"bound": "hbm", "achieved": round(b / k_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(b / k_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "gemv"}}
+                         "frac": round(b / k_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "gemv1"}}
         log(f"[bench] dense: head {ds3.TYPE_NAMES[t]} {k_s * 1e6:.1f} us ({b / k_s / 1e12:.2f} TB/s)")
         if t == ds3.TYPE_Q6_K and not args.no_cpu:
             sys.path.insert(0, str(ROOT / "tests"))

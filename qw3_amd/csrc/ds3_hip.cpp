@@ -551,7 +551,7 @@ static int vec_matmul_typed(const ds3_hip_buffer_t *x, const ds3_hip_buffer_t *W
     if (!fits(x, (size_t)in_dim * 4, "x") || !fits(y, (size_t)out_dim * 4, "y") ||
         !fits(W, (size_t)(out_dim - 1) * row_stride + (size_t)row_stride, "W"))
         return -1;
-    KScope ks("gemv");
+    KScope ks(gemv1_path(type, cptr(W), row_stride, 1, (int)in_dim) ? "gemv1" : "gemv");
     return finish(launch_gemv(type, (const float *)dptr(x), in_dim, cptr(W), row_stride, fptr(y), out_dim, 1,
                               (int)out_dim, (int)in_dim, nullptr, g.stream),
                   what);
@@ -615,7 +615,7 @@ extern "C" int ds3_hip_vec_matmul_q4k_half(const ds3_hip_buffer_t *x, const ds3_
         e = launch_to_f32((const _Float16 *)dptr(x), (float *)ws, in_dim, g.stream);
     }
     if (e == hipSuccess) {
-        KScope ks("gemv");
+        KScope ks(gemv1_path(T_Q4_K, cptr(W), row_stride, 1, (int)in_dim) ? "gemv1" : "gemv");
         e = launch_gemv(T_Q4_K, (const float *)ws, in_dim, cptr(W), row_stride, fptr(y), out_dim, 1, (int)out_dim,
                         (int)in_dim, nullptr, g.stream);
     }
@@ -705,7 +705,7 @@ extern "C" int ds3_hip_matmul_quantized_batch(const ds3_hip_buffer_t *A, const d
         }
         return finish(e, "matmul_quantized_batch");
     }
-    KScope ks("gemv");
+    KScope ks(gemv1_path(type, cptr(W) + weight_offset, weight_row_stride, (int)M, (int)K) ? "gemv1" : "gemv");
     return finish(launch_gemv(type, fptr(A), K, cptr(W) + weight_offset, weight_row_stride, fptr(C), N, (int)M,
                               (int)N, (int)K, nullptr, g.stream),
                   "matmul_quantized_batch");

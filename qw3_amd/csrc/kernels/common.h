@@ -35,19 +35,21 @@ __device__ __forceinline__ float h2f(uint32_t bits16)
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
 
 // Read 4 bytes at a 2-byte-aligned address with dword-aligned loads only.
+// The aligned address is p minus its low bits as pointer arithmetic, not an
+// integer mask, so a pointer into LDS stays an LDS pointer (ds_read, not a
+// flat load, which would also count against vmcnt).
 __device__ __forceinline__ uint32_t ld_u32_a2(const uint8_t *p)
 {
-    const uintptr_t a = (uintptr_t)p;
-    const uint32_t *q = (const uint32_t *)(a & ~(uintptr_t)3);
-    return __builtin_amdgcn_alignbyte(q[1], q[0], (uint32_t)(a & 3));
+    const uint32_t s = (uint32_t)((uintptr_t)p & 3);
+    const uint32_t *q = (const uint32_t *)(p - s);
+    return __builtin_amdgcn_alignbyte(q[1], q[0], s);
 }
 
 // Read 8 bytes at a 2-byte-aligned address (3 dword loads + 2 funnel shifts).
 __device__ __forceinline__ uint2 ld_u64_a2(const uint8_t *p)
 {
-    const uintptr_t a = (uintptr_t)p;
-    const uint32_t *q = (const uint32_t *)(a & ~(uintptr_t)3);
-    const uint32_t s = (uint32_t)(a & 3);
+    const uint32_t s = (uint32_t)((uintptr_t)p & 3);
+    const uint32_t *q = (const uint32_t *)(p - s);
     const uint32_t w0 = q[0], w1 = q[1], w2 = q[2];
     return make_uint2(__builtin_amdgcn_alignbyte(w1, w0, s), __builtin_amdgcn_alignbyte(w2, w1, s));
 }

@@ -4,10 +4,233 @@
 // matmul_quantized_batch entry points (src/ds3_metal.h:90-161) and the router
 // logits.  Lanes split K in 32-weight units; a group of G lanes owns one row
 // and decodes each unit once for a tile of up to 8 tokens staged in LDS.
+//
+// One token over long matrices (the output head, 151,936 x 2048, and the
+// decode projections, src/ds3_engine.c:181-247) goes to k_gemv1 instead: the
+// rows stream as one contiguous byte range per chunk of rows, not as the
+// scattered unit loads of k_gemv.
 #include "common.h"
 #include "launch.h"
 
 namespace ds3k {
+
+// ---------------------------------------------------------------------------
+// k_gemv1: y[n] = x . W[n] for one token, Q4_K / Q6_K / Q8_0 rows of
+// K = 2048 * UPL weights stored densely (row stride = row bytes) from a
+// 16-byte aligned base.  Persistent workgroups walk chunks of R consecutive
+// rows, one contiguous byte range each.  Every thread loads 16-byte pieces of
+// a chunk into one of two register sets (inline asm loads, waited by an asm
+// s_waitcnt after which every register of the set is named), so one chunk is
+// always in flight while the other is decoded.  A landed chunk goes to one of
+// two LDS buffers; each wave takes R/4 of its rows, each lane decodes units
+// lane + 64 q of a row from LDS against its x values, which stay in registers
+// for the whole kernel (loaded once per workgroup), and a DPP wave sum gives
+// the row's product.
+// ---------------------------------------------------------------------------
+bool gemv_type_ok(int type, int K);
+
+constexpr int G1_TPB = 256;
+constexpr int G1_LOAD = G1_TPB * 16;            // bytes one load instruction of the workgroup covers
+
+template <int TYPE> struct G1Row;               // row bytes per 2048 weights
+template <> struct G1Row<T_Q4_K> { static constexpr int RB = 1152; };
+template <> struct G1Row<T_Q6_K> { static constexpr int RB = 1680; };
+template <> struct G1Row<T_Q8_0> { static constexpr int RB = 2176; };
+
+template <int TYPE, int UPL>
+struct G1 {
+    static constexpr int RB = G1Row<TYPE>::RB * UPL;             // bytes per row
+    static constexpr int R = 16 / UPL;                           // rows per chunk
+    static constexpr int CB = R * RB;                            // chunk bytes
+    static constexpr int NL = (CB + G1_LOAD - 1) / G1_LOAD;      // 16-byte loads per thread and chunk
+    static constexpr int BUF = NL * G1_LOAD;                     // LDS bytes per buffer
+    static_assert(R % 4 == 0 && RB % 16 == 0, "whole rows per wave, 16-byte rows");
+};
+
+typedef uint32_t g1_u32x4 __attribute__((ext_vector_type(4)));
+
+template <int NL>
+struct G1Set {
+    g1_u32x4 v[NL];
+    // the chunk at byte offset off0; pieces past the tensor's last 16 bytes
+    // (the last chunk's missing rows) re-read those bytes and are never used
+    __device__ __forceinline__ void issue(const uint8_t *base, int64_t off0, int64_t lim)
+    {
+#pragma unroll
+        for (int l = 0; l < NL; l++) {
+            int64_t o = off0 + 16 * (int64_t)threadIdx.x + (int64_t)G1_LOAD * l;
+            if (o > lim) o = lim;
+            asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v[l]) : "v"(base + o) : "memory");
+        }
+    }
+    // wait until at most N loads issued after this set's are outstanding
+    template <int N>
+    __device__ __forceinline__ void wait()
+    {
+        static_assert(N <= 63, "vmcnt field holds 0..63");
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+#pragma unroll
+        for (int l = 0; l < NL; l++) asm volatile("" : "+v"(v[l]));
+    }
+    __device__ __forceinline__ void to_lds(uint8_t *buf) const
+    {
+#pragma unroll
+        for (int l = 0; l < NL; l++) *(g1_u32x4 *)(buf + 16 * threadIdx.x + G1_LOAD * l) = v[l];
+    }
+};
+
+// K positions of unit u's weights in unit_decode's order: w[8s + i] pairs
+// with x[k0[s] + i].
+template <int TYPE>
+__device__ __forceinline__ void unit_k0(int u, int (&k0)[4])
+{
+    if constexpr (TYPE == T_Q4_K) {
+        const int b = u >> 3, c = u & 7, kl = 256 * b + 64 * (c >> 1) + 16 * (c & 1);
+        k0[0] = kl; k0[1] = kl + 8; k0[2] = kl + 32; k0[3] = kl + 40;
+    } else if constexpr (TYPE == T_Q6_K) {
+        const int b = u >> 3, h = (u >> 2) & 1, j = u & 3;
+#pragma unroll
+        for (int t = 0; t < 4; t++) k0[t] = 256 * b + 128 * h + 32 * t + 8 * j;
+    } else {
+#pragma unroll
+        for (int s = 0; s < 4; s++) k0[s] = 32 * u + 8 * s;
+    }
+}
+
+// Sum over the wavefront with the total in lane 63 (DPP, no LDS round trip):
+// two quad swaps and row rotations by 4 and 8 leave every lane of a 16-lane
+// row with the row's sum; row_bcast:15 adds row 0 into row 1 and row 2 into
+// row 3, row_bcast:31 rows 0-1 into row 3.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float g1_dpp(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+__device__ __forceinline__ float g1_wave_total(float v)
+{
+    v = v + g1_dpp<0xB1>(v);           // quad_perm [1,0,3,2]
+    v = v + g1_dpp<0x4E>(v);           // quad_perm [2,3,0,1]
+    v = v + g1_dpp<0x124>(v);          // row_ror:4
+    v = v + g1_dpp<0x128>(v);          // row_ror:8
+    v = v + g1_dpp<0x142, 0xa>(v);     // row_bcast:15
+    v = v + g1_dpp<0x143, 0xc>(v);     // row_bcast:31
+    return v;
+}
+
+template <int TYPE, int UPL>
+__global__ void __launch_bounds__(G1_TPB)
+k_gemv1(const float *__restrict__ x, const uint8_t *__restrict__ W, float *__restrict__ y, int N, int nch)
+{
+    using P = G1<TYPE, UPL>;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * P::BUF];
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    float xr[UPL][32];
+#pragma unroll
+    for (int q = 0; q < UPL; q++) {
+        int k0[4];
+        unit_k0<TYPE>(lane + 64 * q, k0);
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) xr[q][8 * s + i] = x[k0[s] + i];
+    }
+    // x has landed before the first chunk's loads go out: the compiler's own
+    // wait for x (it does not see the asm loads) then waits for x alone
+#pragma unroll
+    for (int q = 0; q < UPL; q++)
+#pragma unroll
+        for (int m = 0; m < 32; m++) asm volatile("" ::"v"(xr[q][m]));
+    auto compute = [&](const uint8_t *buf, int c) {
+        // one row at a time: four rows' decoded weights at once cost the second wave per SIMD
+#pragma unroll 1
+        for (int i = 0; i < P::R / 4; i++) {
+            const int r = wave + 4 * i;
+            float acc = 0.f;
+#pragma unroll
+            for (int q = 0; q < UPL; q++) {
+                float w[32];
+                int k0[4];
+                unit_decode<TYPE>(buf + r * P::RB, lane + 64 * q, w, k0);
+#pragma unroll
+                for (int m = 0; m < 32; m++) acc = fmaf(w[m], xr[q][m], acc);
+            }
+            acc = g1_wave_total(acc);
+            const int n = c * P::R + r;
+            if (lane == WAVE - 1 && n < N) y[n] = acc;
+        }
+    };
+    const int G = (int)gridDim.x;
+    int c = (int)blockIdx.x;
+    const int64_t lim = (int64_t)N * P::RB - 16;
+    G1Set<P::NL> A, B;
+    A.issue(W, (int64_t)c * P::CB, lim);
+    B.issue(W, (int64_t)min(c + G, nch - 1) * P::CB, lim);
+    for (;;) {
+        A.template wait<P::NL>();                     // B's loads went out after A's
+        A.to_lds(lds);
+        __syncthreads();                              // every wave is done with buffer 0's previous chunk
+        A.issue(W, (int64_t)min(c + 2 * G, nch - 1) * P::CB, lim);
+        compute(lds, c);
+        if (c + G >= nch) break;                      // uniform over the workgroup
+        B.template wait<P::NL>();                     // A's loads went out after B's
+        B.to_lds(lds + P::BUF);
+        __syncthreads();
+        B.issue(W, (int64_t)min(c + 3 * G, nch - 1) * P::CB, lim);
+        compute(lds + P::BUF, c + G);
+        c += 2 * G;
+        if (c >= nch) break;
+    }
+    // both sets still have loads in flight: wait for them, naming the registers
+    A.template wait<0>();
+    B.template wait<0>();
+}
+
+template <int TYPE, int UPL>
+static hipError_t gemv1_t(const float *x, const uint8_t *w, float *y, int N, hipStream_t s)
+{
+    static int n_cu = 0;
+    if (n_cu == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+            n_cu = 256;
+    }
+    const int nch = (N + G1<TYPE, UPL>::R - 1) / G1<TYPE, UPL>::R;
+    const int grid = nch < 2 * n_cu ? nch : 2 * n_cu;
+    hipLaunchKernelGGL((k_gemv1<TYPE, UPL>), dim3((unsigned)grid), dim3(G1_TPB), 0, s, x, w, y, N, nch);
+    return hipGetLastError();
+}
+
+// k_gemv1's shapes: one token, Q4_K / Q6_K / Q8_0, K = 2048 or 4096, dense
+// rows from a 16-byte aligned base.
+static bool gemv1_ok(int type, const uint8_t *w, uint64_t stride, int M, int K, const float *wnorm2)
+{
+    if (M != 1 || wnorm2 != nullptr || (K != 2048 && K != 4096) || ((uintptr_t)w & 15) != 0) return false;
+    const int upl = K / 2048;
+    switch (type) {
+    case T_Q4_K: return stride == (uint64_t)G1Row<T_Q4_K>::RB * upl;
+    case T_Q6_K: return stride == (uint64_t)G1Row<T_Q6_K>::RB * upl;
+    case T_Q8_0: return stride == (uint64_t)G1Row<T_Q8_0>::RB * upl;
+    default: return false;
+    }
+}
+
+bool gemv1_path(int type, const uint8_t *w, uint64_t stride, int M, int K)
+{
+    return gemv_type_ok(type, K) && gemv1_ok(type, w, stride, M, K, nullptr);
+}
+
+static hipError_t launch_gemv1(int type, const float *x, const uint8_t *w, float *y, int N, int K, hipStream_t s)
+{
+    const bool two = K == 4096;
+    switch (type) {
+    case T_Q4_K: return two ? gemv1_t<T_Q4_K, 2>(x, w, y, N, s) : gemv1_t<T_Q4_K, 1>(x, w, y, N, s);
+    case T_Q6_K: return two ? gemv1_t<T_Q6_K, 2>(x, w, y, N, s) : gemv1_t<T_Q6_K, 1>(x, w, y, N, s);
+    case T_Q8_0: return two ? gemv1_t<T_Q8_0, 2>(x, w, y, N, s) : gemv1_t<T_Q8_0, 1>(x, w, y, N, s);
+    default: return hipErrorInvalidValue;
+    }
+}
 
 constexpr int GEMV_MT = 8;            // tokens per tile
 constexpr int GEMV_TPB = 256;
@@ -119,6 +342,7 @@ hipError_t launch_gemv(int type, const float *A, int64_t lda, const uint8_t *w, 
                        float *C, int64_t ldc, int M, int N, int K, float *wnorm2, hipStream_t s)
 {
     if (!gemv_type_ok(type, K) || M <= 0 || N <= 0) return hipErrorInvalidValue;
+    if (gemv1_ok(type, w, stride, M, K, wnorm2)) return launch_gemv1(type, A, w, C, N, K, s);
     const int G = lanes_per_row(K / 32);
     const int gpw = WAVE / G;
     const int rows_step = (GEMV_TPB / WAVE) * gpw;            // rows one pass of the WG covers

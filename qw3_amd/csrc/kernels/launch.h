@@ -28,6 +28,10 @@ hipError_t launch_gemv(int type, const float *A, int64_t lda, const uint8_t *w, 
                        float *C, int64_t ldc, int M, int N, int K, float *wnorm2, hipStream_t s);
 
 bool gemv_type_ok(int type, int K);
+// Whether launch_gemv takes its one-token chunked path (k_gemv1) for these
+// arguments: M = 1, Q4_K / Q6_K / Q8_0, K = 2048 or 4096, dense rows, w
+// 16-byte aligned, no wnorm2.
+bool gemv1_path(int type, const uint8_t *w, uint64_t stride, int M, int K);
 
 // Router tail: logits [T][E] -> softmax -> top-k -> renorm, selected by
 // (prob desc, index asc) like the reference.

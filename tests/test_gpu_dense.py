@@ -97,6 +97,72 @@ def test_matmul_quantized_batch_paths(hip_ready):
         hip().ds3_hip_set_dense_mfma_min_rows(prev)
 
 
+SIMD_NAME = {12: "q4k", 14: "q6k", 8: "q8_0"}
+
+
+def vec_matmul_kernel(t, xb, wb, yb, K, N, stride):
+    """One vec_matmul call with kernel timing on; returns the kernels it ran."""
+    hip().ds3_hip_kernel_timing_reset()
+    hip().ds3_hip_kernel_timing(1)
+    rc = hip().ds3_hip_vec_matmul_quantized(xb, wb, yb, K, N, stride, t)
+    hip().ds3_hip_kernel_timing(0)
+    assert rc == 0
+    return kernels_run()
+
+
+@pytest.mark.parametrize("t,N,K", [(12, 1031, 2048), (14, 4099, 4096), (8, 333, 4096), (8, 16, 2048),
+                                   (14, 1, 2048), (12, 17, 4096), (14, 40, 2048), (8, 9, 4096)])
+def test_vec_matmul_one_token_path(hip_ready, t, N, K):
+    """One token against dense, 16-byte aligned Q4_K / Q6_K / Q8_0 rows of
+    K = 2048 or 4096 runs on the chunked one-token kernel (gemv1): row counts
+    that leave a partial last chunk, a single row, and fewer rows than one
+    chunk; the reference's tolerance, 1e-4 (tests/test_matmul_quant_metal.c:66)."""
+    x = np.random.default_rng(N + K).standard_normal(K).astype(np.float32)
+    raw = normal_matrix(t, 11, N, K)
+    want = O.vec_matmul(x, O.dequantize(t, raw, N * K).reshape(N, K))
+    yb = ds3.Buffer.alloc(N * 4)
+    print(f"  gemv1 {ds3.TYPE_NAMES[t]} N={N} K={K}", flush=True)
+    ran = vec_matmul_kernel(t, ds3.Buffer.from_array(x), ds3.Buffer.from_array(raw), yb, K, N, ds3.row_bytes(t, K))
+    assert "gemv1" in ran and "gemv" not in ran
+    err = float(np.abs(yb.read(np.float32, N) - want).max())
+    print(f"    max_abs={err:.2e}", flush=True)
+    assert err < TOL_FP32
+
+
+def test_vec_matmul_one_token_fallbacks(hip_ready):
+    """Rows the chunked kernel does not take go to the general kernel, with
+    the same results: a weight base 8 bytes past a 16-byte boundary, rows
+    padded past their bytes, and K outside {2048, 4096}."""
+    t, N, K = 14, 300, 2048
+    rb = ds3.row_bytes(t, K)
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(K).astype(np.float32)
+    raw = normal_matrix(t, 12, N, K)
+    want = O.vec_matmul(x, O.dequantize(t, raw, N * K).reshape(N, K))
+    xb, yb = ds3.Buffer.from_array(x), ds3.Buffer.alloc(N * 4)
+    # base 8 bytes off
+    big = ds3.Buffer.alloc(raw.nbytes + 8)
+    big.write(raw, offset=8)
+    ran = vec_matmul_kernel(t, xb, big.view(8, raw.nbytes), yb, K, N, rb)
+    assert "gemv" in ran and "gemv1" not in ran
+    assert float(np.abs(yb.read(np.float32, N) - want).max()) < TOL_FP32
+    # padded rows: 32 spare bytes per row
+    pad = np.zeros((N, rb + 32), np.uint8)
+    pad[:, :rb] = raw.reshape(N, rb)
+    yb.zero()
+    ran = vec_matmul_kernel(t, xb, ds3.Buffer.from_array(pad), yb, K, N, rb + 32)
+    assert "gemv" in ran and "gemv1" not in ran
+    assert float(np.abs(yb.read(np.float32, N) - want).max()) < TOL_FP32
+    # K = 1024
+    K2 = 1024
+    raw2 = normal_matrix(t, 13, N, K2)
+    want2 = O.vec_matmul(x[:K2], O.dequantize(t, raw2, N * K2).reshape(N, K2))
+    ran = vec_matmul_kernel(t, ds3.Buffer.from_array(x[:K2]), ds3.Buffer.from_array(raw2), yb, K2, N,
+                            ds3.row_bytes(t, K2))
+    assert "gemv" in ran and "gemv1" not in ran
+    assert float(np.abs(yb.read(np.float32, N) - want2).max()) < TOL_FP32
+
+
 @pytest.mark.parametrize("t", [14, 8])
 def test_output_head_vec_matmul(hip_ready, t):
     """The engine's output projection (dispatch_output_matmul, reference
@@ -111,11 +177,11 @@ def test_output_head_vec_matmul(hip_ready, t):
     xb = ds3.Buffer.from_array(x)
     yb = ds3.Buffer.alloc(HEAD_N * 4)
     rs = ds3.row_bytes(t, K)
-    assert hip().ds3_hip_vec_matmul_quantized(xb, wb, yb, K, HEAD_N, rs, t) == 0
+    assert "gemv1" in vec_matmul_kernel(t, xb, wb, yb, K, HEAD_N, rs)      # the one-token chunked kernel
     err = float(np.abs(yb.read(np.float32, HEAD_N) - want).max())
     print(f"    max_abs={err:.2e}", flush=True)
     assert err < TOL_FP32
-    simd = {14: "q6k", 8: "q8_0"}[t]
+    simd = SIMD_NAME[t]
     yb.zero()
     assert getattr(hip(), f"ds3_hip_vec_matmul_{simd}_simd")(xb, wb, yb, K, HEAD_N, rs) == 0
     assert float(np.abs(yb.read(np.float32, HEAD_N) - want).max()) < TOL_FP32
