@@ -22,10 +22,10 @@ namespace ds3k {
 // a chunk into one of two register sets (inline asm loads, waited by an asm
 // s_waitcnt after which every register of the set is named), so one chunk is
 // always in flight while the other is decoded.  A landed chunk goes to one of
-// two LDS buffers; each wave takes R/4 of its rows, each lane decodes units
-// lane + 64 q of a row from LDS against its x values, which stay in registers
-// for the whole kernel (loaded once per workgroup), and a DPP wave sum gives
-// the row's product.
+// two LDS buffers; each wave takes R/4 of its rows, each lane dots units
+// lane + 64 q of a row from LDS with its x values, which stay in registers
+// for the whole kernel with their 8-element sums (loaded once per
+// workgroup), and a DPP wave sum gives the row's product.
 // ---------------------------------------------------------------------------
 bool gemv_type_ok(int type, int K);
 
@@ -37,10 +37,17 @@ template <> struct G1Row<T_Q4_K> { static constexpr int RB = 1152; };
 template <> struct G1Row<T_Q6_K> { static constexpr int RB = 1680; };
 template <> struct G1Row<T_Q8_0> { static constexpr int RB = 2176; };
 
+#ifndef DS3_G1_ROWS
+#define DS3_G1_ROWS 8               // rows per chunk at K = 2048 (half at 4096)
+#endif
+#ifndef DS3_G1_WPC
+#define DS3_G1_WPC 4                // persistent workgroups per CU
+#endif
+
 template <int TYPE, int UPL>
 struct G1 {
     static constexpr int RB = G1Row<TYPE>::RB * UPL;             // bytes per row
-    static constexpr int R = 16 / UPL;                           // rows per chunk
+    static constexpr int R = DS3_G1_ROWS / UPL;                  // rows per chunk
     static constexpr int CB = R * RB;                            // chunk bytes
     static constexpr int NL = (CB + G1_LOAD - 1) / G1_LOAD;      // 16-byte loads per thread and chunk
     static constexpr int BUF = NL * G1_LOAD;                     // LDS bytes per buffer
@@ -118,6 +125,66 @@ __device__ __forceinline__ float g1_wave_total(float v)
     return v;
 }
 
+// One unit's dot with this lane's x values in unit_decode's order (xv[8s +
+// i] pairs with the unit's weight 8s + i), factored like the reference's
+// block dots: codes against x, then each sub-block's scale and offset once.
+// sx[s] = xv[8s] + ... + xv[8s + 7], the same for every row, so it is
+// computed once per lane.
+template <int TYPE>
+__device__ __forceinline__ float g1_unit_dot(const uint8_t *row, int u, const float (&xv)[32], const float (&sx)[4])
+{
+    if constexpr (TYPE == T_Q4_K) {
+        const int b = u >> 3, c = u & 7;
+        const uint8_t *blk = row + b * 144;
+        const uint4 hdr = *(const uint4 *)blk;
+        const uint4 q = *(const uint4 *)(blk + 16 + 16 * c);
+        const float d = h2f(hdr.x & 0xffffu), dmin = h2f(hdr.x >> 16);
+        float sc0, mn0, sc1, mn1;
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1), sc0, mn0);
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1) + 1, sc1, mn1);
+        const uint32_t qw[4] = { q.x, q.y, q.z, q.w };
+        float dl = 0.f, dh = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            dl += dot4(qw[i] & 0x0f0f0f0fu, xv + 4 * i);
+            dh += dot4((qw[i] >> 4) & 0x0f0f0f0fu, xv + 16 + 4 * i);
+        }
+        return (d * sc0) * dl - (dmin * mn0) * (sx[0] + sx[1]) + (d * sc1) * dh - (dmin * mn1) * (sx[2] + sx[3]);
+    } else if constexpr (TYPE == T_Q6_K) {
+        const int b = u >> 3, h = (u >> 2) & 1, j = u & 3;
+        const uint8_t *blk = row + b * 210;
+        const uint2 lo = ld_u64_a2(blk + 64 * h + 8 * j);
+        const uint2 hi = ld_u64_a2(blk + 64 * h + 32 + 8 * j);
+        const uint2 qh = ld_u64_a2(blk + 128 + 32 * h + 8 * j);
+        const uint2 scw = ld_u64_a2(blk + 192 + 8 * h);
+        const float d = h2f(ld_u16(blk + 208));
+        const int s0 = j >> 1;
+        const uint32_t low[2] = { lo.x, lo.y }, hig[2] = { hi.x, hi.y }, hb[2] = { qh.x, qh.y };
+        float acc = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float sc = (float)(int8_t)byte_of(t < 2 ? scw.x : scw.y, (s0 + 2 * t) & 3);
+            float dc = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < 2; ww++) {
+                const uint32_t ql = (t & 1) ? hig[ww] : low[ww];
+                const uint32_t nib = (t < 2) ? (ql & 0x0f0f0f0fu) : ((ql >> 4) & 0x0f0f0f0fu);
+                dc += dot4(nib | (((hb[ww] >> (2 * t)) & 0x03030303u) << 4), xv + 8 * t + 4 * ww);
+            }
+            acc += sc * (dc - 32.f * sx[t]);
+        }
+        return d * acc;
+    } else {
+        static_assert(TYPE == T_Q8_0, "Q4_K, Q6_K or Q8_0");
+        const uint8_t *blk = row + u * 34;
+        const float d = h2f(ld_u16(blk));
+        float dc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) dc += dot4(ld_u32_a2(blk + 2 + 4 * i) ^ 0x80808080u, xv + 4 * i);   // int8 + 128
+        return d * (dc - 128.f * ((sx[0] + sx[1]) + (sx[2] + sx[3])));
+    }
+}
+
 template <int TYPE, int UPL>
 __global__ void __launch_bounds__(G1_TPB)
 k_gemv1(const float *__restrict__ x, const uint8_t *__restrict__ W, float *__restrict__ y, int N, int nch)
@@ -135,12 +202,22 @@ k_gemv1(const float *__restrict__ x, const uint8_t *__restrict__ W, float *__res
 #pragma unroll
             for (int i = 0; i < 8; i++) xr[q][8 * s + i] = x[k0[s] + i];
     }
+    float sx[UPL][4];
+#pragma unroll
+    for (int q = 0; q < UPL; q++)
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            float t = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) t += xr[q][8 * s + i];
+            sx[q][s] = t;
+        }
     // x has landed before the first chunk's loads go out: the compiler's own
     // wait for x (it does not see the asm loads) then waits for x alone
 #pragma unroll
     for (int q = 0; q < UPL; q++)
 #pragma unroll
-        for (int m = 0; m < 32; m++) asm volatile("" ::"v"(xr[q][m]));
+        for (int s = 0; s < 4; s++) asm volatile("" ::"v"(sx[q][s]));
     auto compute = [&](const uint8_t *buf, int c) {
         // one row at a time: four rows' decoded weights at once cost the second wave per SIMD
 #pragma unroll 1
@@ -148,13 +225,7 @@ k_gemv1(const float *__restrict__ x, const uint8_t *__restrict__ W, float *__res
             const int r = wave + 4 * i;
             float acc = 0.f;
 #pragma unroll
-            for (int q = 0; q < UPL; q++) {
-                float w[32];
-                int k0[4];
-                unit_decode<TYPE>(buf + r * P::RB, lane + 64 * q, w, k0);
-#pragma unroll
-                for (int m = 0; m < 32; m++) acc = fmaf(w[m], xr[q][m], acc);
-            }
+            for (int q = 0; q < UPL; q++) acc += g1_unit_dot<TYPE>(buf + r * P::RB, lane + 64 * q, xr[q], sx[q]);
             acc = g1_wave_total(acc);
             const int n = c * P::R + r;
             if (lane == WAVE - 1 && n < N) y[n] = acc;
@@ -197,7 +268,7 @@ static hipError_t gemv1_t(const float *x, const uint8_t *w, float *y, int N, hip
             n_cu = 256;
     }
     const int nch = (N + G1<TYPE, UPL>::R - 1) / G1<TYPE, UPL>::R;
-    const int grid = nch < 2 * n_cu ? nch : 2 * n_cu;
+    const int grid = nch < DS3_G1_WPC * n_cu ? nch : DS3_G1_WPC * n_cu;
     hipLaunchKernelGGL((k_gemv1<TYPE, UPL>), dim3((unsigned)grid), dim3(G1_TPB), 0, s, x, w, y, N, nch);
     return hipGetLastError();
 }
