@@ -19,10 +19,10 @@ namespace ds3k {
 // K = 2048 * UPL weights stored densely (row stride = row bytes) from a
 // 16-byte aligned base.  Persistent workgroups walk chunks of R consecutive
 // rows, one contiguous byte range each.  Every thread loads 16-byte pieces of
-// a chunk into one of two register sets (inline asm loads, waited by an asm
-// s_waitcnt after which every register of the set is named), so one chunk is
-// always in flight while the other is decoded.  A landed chunk goes to one of
-// two LDS buffers; each wave takes R/4 of its rows, each lane dots units
+// a chunk into one of NS register sets in rotation (inline asm loads, waited
+// by an asm s_waitcnt after which every register of the set is named), so
+// NS - 1 chunks are in flight while one is decoded.  A landed chunk goes to
+// one of two LDS buffers; each wave takes R/4 of its rows, each lane dots units
 // lane + 64 q of a row from LDS with its x values, which stay in registers
 // for the whole kernel with their 8-element sums (loaded once per
 // workgroup), and a DPP wave sum gives the row's product.
@@ -43,6 +43,9 @@ template <> struct G1Row<T_Q8_0> { static constexpr int RB = 2176; };
 #ifndef DS3_G1_WPC
 #define DS3_G1_WPC 4                // persistent workgroups per CU
 #endif
+#ifndef DS3_G1_SETS
+#define DS3_G1_SETS 2               // register sets of chunks in flight per workgroup
+#endif
 
 template <int TYPE, int UPL>
 struct G1 {
@@ -59,13 +62,17 @@ typedef uint32_t g1_u32x4 __attribute__((ext_vector_type(4)));
 template <int NL>
 struct G1Set {
     g1_u32x4 v[NL];
-    // the chunk at byte offset off0; pieces past the tensor's last 16 bytes
-    // (the last chunk's missing rows) re-read those bytes and are never used
-    __device__ __forceinline__ void issue(const uint8_t *base, int64_t off0, int64_t lim)
+    // the chunk of cb bytes at byte offset off0.  Pieces past the chunk (the
+    // last round of loads overshoots it) re-read its first 16 bytes, a line
+    // the same instruction fetches anyway, instead of the next chunk's lines,
+    // which another workgroup loads; pieces past the tensor's last 16 bytes
+    // (the last chunk's missing rows) re-read those.  Neither is used.
+    __device__ __forceinline__ void issue(const uint8_t *base, int64_t off0, int cb, int64_t lim)
     {
 #pragma unroll
         for (int l = 0; l < NL; l++) {
-            int64_t o = off0 + 16 * (int64_t)threadIdx.x + (int64_t)G1_LOAD * l;
+            const int rel = 16 * (int)threadIdx.x + G1_LOAD * l;
+            int64_t o = off0 + (rel < cb ? rel : 0);
             if (o > lim) o = lim;
             asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v[l]) : "v"(base + o) : "memory");
         }
@@ -234,27 +241,33 @@ k_gemv1(const float *__restrict__ x, const uint8_t *__restrict__ W, float *__res
     const int G = (int)gridDim.x;
     int c = (int)blockIdx.x;
     const int64_t lim = (int64_t)N * P::RB - 16;
-    G1Set<P::NL> A, B;
-    A.issue(W, (int64_t)c * P::CB, lim);
-    B.issue(W, (int64_t)min(c + G, nch - 1) * P::CB, lim);
-    for (;;) {
-        A.template wait<P::NL>();                     // B's loads went out after A's
-        A.to_lds(lds);
-        __syncthreads();                              // every wave is done with buffer 0's previous chunk
-        A.issue(W, (int64_t)min(c + 2 * G, nch - 1) * P::CB, lim);
-        compute(lds, c);
-        if (c + G >= nch) break;                      // uniform over the workgroup
-        B.template wait<P::NL>();                     // A's loads went out after B's
-        B.to_lds(lds + P::BUF);
-        __syncthreads();
-        B.issue(W, (int64_t)min(c + 3 * G, nch - 1) * P::CB, lim);
-        compute(lds + P::BUF, c + G);
-        c += 2 * G;
-        if (c >= nch) break;
+    // NS register sets in rotation: chunk k of this workgroup (c = blockIdx.x
+    // + k G) loads into set k mod NS, NS - 1 chunks ahead of the one being
+    // decoded, and goes to LDS buffer k mod 2
+    constexpr int NS = DS3_G1_SETS;
+    static_assert(NS >= 2 && (NS - 1) * P::NL <= 63, "register sets in flight vs the vmcnt field");
+    G1Set<P::NL> S[NS];
+#pragma unroll
+    for (int j = 0; j < NS; j++) S[j].issue(W, (int64_t)min(c + j * G, nch - 1) * P::CB, P::CB, lim);
+    bool more = true;
+    for (int k = 0; more; k += NS) {
+#pragma unroll
+        for (int j = 0; j < NS; j++) {
+            if (more) {                                   // uniform over the workgroup
+                S[j].template wait<(NS - 1) * P::NL>();   // the other sets' loads went out after this one's
+                uint8_t *buf = lds + ((k + j) & 1) * P::BUF;
+                S[j].to_lds(buf);
+                __syncthreads();                          // every wave is done with this buffer's previous chunk
+                S[j].issue(W, (int64_t)min(c + NS * G, nch - 1) * P::CB, P::CB, lim);
+                compute(buf, c);
+                c += G;
+                more = c < nch;
+            }
+        }
     }
-    // both sets still have loads in flight: wait for them, naming the registers
-    A.template wait<0>();
-    B.template wait<0>();
+    // every set still has loads in flight: wait for them, naming the registers
+#pragma unroll
+    for (int j = 0; j < NS; j++) S[j].template wait<0>();
 }
 
 template <int TYPE, int UPL>
