@@ -365,7 +365,7 @@ def make_layers(spec, n, what):
     hosts, layers = [], []
     for l in range(n):
         h = W.make_layer(spec, seed=1234, layer=l)
-        layers.append(h.to_device())
+        layers.append(h.to_device(readonly=True))       # as the engine imports mmap'd GGUF weights
         if l == 0:
             hosts.append(h)
     log(f"[bench] {what}: {n} layers generated and resident in {time.perf_counter() - t0:.1f}s")
@@ -576,7 +576,7 @@ def leg_stack(args, traffic, n_used=8):
     hosts, layers = [], []
     for l in range(L):
         h = W.make_layer(spec, seed=1234, layer=l)
-        layers.append(h.to_device())
+        layers.append(h.to_device(readonly=True))       # as the engine imports mmap'd GGUF weights
         if l < 2 and not args.no_cpu:
             hosts.append(h)
     log(f"[bench] c4: {L} layers generated and resident in {time.perf_counter() - t0:.1f}s "
@@ -801,7 +801,7 @@ def main():
     }
     if not args.no_t1 and config == 2:
         spec1 = W.config_spec(1)
-        layers1 = [W.make_layer(spec1, seed=1234, layer=l).to_device() for l in range(args.layers)]
+        layers1 = [W.make_layer(spec1, seed=1234, layer=l).to_device(readonly=True) for l in range(args.layers)]
         x1h = [W.make_inputs(1, 1, seed=98, step=s) for s in range(16)]
         x1 = [ds3.Buffer.from_array(x) for x in x1h]
         # decode: the timed steps replay a HIP graph of 16 steps (every layer

@@ -63,6 +63,7 @@ struct State {
     hipStream_t stream = nullptr;
     bool batch = false;
     bool capturing = false;          // between ds3_hip_graph_begin and ds3_hip_graph_end
+    bool no_alloc = false;           // inside ds3_hip_moe_ffn_batch_noalloc: nothing may allocate
     uint8_t *ws = nullptr;
     size_t ws_bytes = 0;
     std::vector<void *> graphs;      // live executable graphs (graph_end .. graph_destroy)
@@ -93,6 +94,17 @@ struct State {
     std::vector<double> stat_ms;
     bool stats_dirty = true;
     hipEvent_t t0 = nullptr, t1 = nullptr;
+    // FP32 copies of non-F32 routers held in read-only buffers (see
+    // router_f32_rows), kept until the owning buffer is freed.
+    struct RouterF32 {
+        const uint8_t *rows;     // the router rows as passed
+        const uint8_t *alloc;    // the allocation holding them (its free drops the copy)
+        int rtype;
+        uint32_t E, K;
+        uint64_t stride;
+        float *f32;              // [E][K]
+    };
+    std::vector<RouterF32> router_f32;
     // The bucketing lists of the last chunk of the last grouped-path call
     // (device pointers into that call's workspace), for
     // ds3_hip_debug_grouped_lists; cleared when the workspace moves.
@@ -193,6 +205,7 @@ void free_retired()
 bool graph_live(void *graph) { return std::find(g.graphs.begin(), g.graphs.end(), graph) != g.graphs.end(); }
 
 
+
 struct Bump {
     size_t off = 0;
     size_t take(size_t bytes)
@@ -225,6 +238,51 @@ struct KScope {
         }
     }
 };
+
+// The FP32 rows of a non-F32 router held in a read-only buffer (the engine's
+// mmap'd weights, ds3_hip_buffer_from_mmap), expanded once and kept until that
+// buffer is freed: its bytes cannot change (buffer_write refuses it), so every
+// later call skips the per-call expansion.  nullptr: the caller expands per
+// call (an F32 router, a writable buffer, or no copy yet during a capture or
+// an allocation-free call).
+const float *router_f32_rows(const ds3_hip_buffer_t *router, int rtype, uint32_t E, uint32_t K, uint64_t stride)
+{
+    if (rtype == T_F32 || !router->readonly) return nullptr;
+    const uint8_t *rows = cptr(router);
+    for (const State::RouterF32 &r : g.router_f32)
+        if (r.rows == rows && r.rtype == rtype && r.E == E && r.K == K && r.stride == stride) return r.f32;
+    if (g.capturing || g.no_alloc || !router_seq_type_ok(rtype, (int)K)) return nullptr;
+    float *f = nullptr;
+    if (hipMalloc((void **)&f, (size_t)E * K * 4 + kAllocPad) != hipSuccess) return nullptr;
+    hipError_t e;
+    {
+        KScope ks("router_rows");
+        e = launch_router_rows(rtype, rows, stride, (int)E, (int)K, f, g.stream);
+    }
+    if (e != hipSuccess) {
+        (void)hipStreamSynchronize(g.stream);
+        (void)hipFree(f);
+        return nullptr;
+    }
+    g.router_f32.push_back({ rows, router->base, rtype, E, K, stride, f });
+    return f;
+}
+
+// Drop the router copies made from the allocation at base, which is being
+// freed; while a live graph may read a copy it is retired, not freed.
+void drop_router_f32(const uint8_t *base)
+{
+    auto &v = g.router_f32;
+    for (size_t i = 0; i < v.size();) {
+        if (v[i].alloc != base) {
+            i++;
+            continue;
+        }
+        if (g.graphs.empty()) (void)hipFree(v[i].f32);
+        else g.retired.push_back((uint8_t *)v[i].f32);
+        v.erase(v.begin() + (std::ptrdiff_t)i);
+    }
+}
 
 bool is_quant(int t) { return t == T_Q4_K || t == T_Q6_K || t == T_Q8_0; }
 
@@ -437,6 +495,7 @@ extern "C" void ds3_hip_shutdown(void)
     (void)hipEventDestroy(g.t0);
     (void)hipEventDestroy(g.t1);
     if (g.ws) (void)hipFree(g.ws);
+    for (const State::RouterF32 &r : g.router_f32) (void)hipFree(r.f32);
     (void)hipFree(g.zero_idx);
     (void)hipStreamDestroy(g.stream);
     uint8_t *sd[kMaxDevices];
@@ -509,6 +568,7 @@ extern "C" void ds3_hip_buffer_free(ds3_hip_buffer_t *buf)
     }
     if (buf->owner && buf->base) {
         if (g.inited) (void)hipStreamSynchronize(g.stream);
+        drop_router_f32(buf->base);
         (void)hipFree(buf->base);
     }
     free(buf);
@@ -919,11 +979,18 @@ int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstrid
     ra.logit_stride = n_expert;
     ra.out_stride = n_used;
     ra.norm = norm;
+    // a read-only router's FP32 copy, made once: the routing then reads F32 rows
+    const float *rf = router_f32_rows(router, rtype, n_expert, n_embd, rstride);
+    const uint8_t *rw = rf ? (const uint8_t *)rf : cptr(router);
+    if (rf) {
+        rtype = T_F32;
+        rstride = (uint64_t)n_embd * 4;
+    }
     hipError_t e;
     if (use_cert(x, T, n_embd, n_expert, n_used, allow_cert)) {
         {
             KScope ks("router_sums");
-            e = launch_router_cert(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, rb.wf32,
+            e = launch_router_cert(x, T, (int)n_embd, (int)n_expert, rtype, rw, rstride, rb.wf32,
                                    rb.logits, n_expert, rb.x16, ra, rb.cert, g.cert_stats, 1, g.stream, np);
         }
         if (np != nullptr) x = np->xn;
@@ -932,7 +999,7 @@ int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstrid
             // LDS at K = 2048) keep 3 of its workgroups per CU at T <= 2
             const int rowb = ((int)n_embd + 4) * 4;
             const int nb = std::max(1, std::min(T <= 2 ? DS3_FUSED_NB : 2, 33792 / rowb));
-            e = router_cert_sel(T, (int)n_embd, (int)n_expert, (int)n_used, rtype, cptr(router), rstride, rb.wf32,
+            e = router_cert_sel(T, (int)n_embd, (int)n_expert, (int)n_used, rtype, rw, rstride, rb.wf32,
                                 rb.cert, g.cert_stats, nb, &defer->cs);
             if (e == hipSuccess) {
                 defer->on = true;
@@ -941,12 +1008,12 @@ int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstrid
         } else if (e == hipSuccess) {
             {
                 KScope ks("router_select");
-                e = launch_router_cert(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, rb.wf32,
+                e = launch_router_cert(x, T, (int)n_embd, (int)n_expert, rtype, rw, rstride, rb.wf32,
                                        rb.logits, n_expert, rb.x16, ra, rb.cert, g.cert_stats, 2, g.stream);
             }
             CertSel cs{};
             if (e == hipSuccess && exact != nullptr &&
-                router_cert_sel(T, (int)n_embd, (int)n_expert, (int)n_used, rtype, cptr(router), rstride, rb.wf32,
+                router_cert_sel(T, (int)n_embd, (int)n_expert, (int)n_used, rtype, rw, rstride, rb.wf32,
                                 rb.cert, g.cert_stats, 1, &cs) == hipSuccess)
                 *exact = ExactTail{ cs.w, cs.wstride, ra };
         }
@@ -957,7 +1024,7 @@ int route_tokens(const float *x, const ds3_hip_buffer_t *router, uint64_t rstrid
     bool topk_done = false;
     {
         KScope ks("router_logits");
-        e = launch_router_seq(x, T, (int)n_embd, (int)n_expert, rtype, cptr(router), rstride, rb.wf32, rb.logits,
+        e = launch_router_seq(x, T, (int)n_embd, (int)n_expert, rtype, rw, rstride, rb.wf32, rb.logits,
                               n_expert, rb.x16, &ra, g.tickets, &topk_done, g.stream);
     }
     if (e != hipSuccess) return report(e, "router logits");
@@ -1512,12 +1579,15 @@ extern "C" int ds3_hip_moe_ffn_batch_noalloc(
         !fits(indices, T * n_used * 4, "indices") || !fits(scores, T * n_used * 4, "scores"))
         return -1;
     const WsFixed fx{ g.scratch_dev[g.device], kScratchBytes };
-    return moe_batch(fptr(input), nullptr, w_gate_inp, w_gate_exps, w_up_exps, w_down_exps, gate_type, up_type,
-                     down_type, gate_row_stride, up_row_stride, down_row_stride, expert_offsets, fptr(output),
-                     residual ? fptr(residual) : nullptr, gate_logits ? fptr(gate_logits) : nullptr,
-                     indices ? (int32_t *)dptr(indices) : nullptr, scores ? fptr(scores) : nullptr, n_tokens, n_embd,
-                     n_expert, n_used, n_ff_exp, router_row_stride, router_type, norm_topk_prob,
-                     "moe_ffn_batch_noalloc", &fx);
+    g.no_alloc = true;
+    const int rc = moe_batch(fptr(input), nullptr, w_gate_inp, w_gate_exps, w_up_exps, w_down_exps, gate_type,
+                             up_type, down_type, gate_row_stride, up_row_stride, down_row_stride, expert_offsets,
+                             fptr(output), residual ? fptr(residual) : nullptr,
+                             gate_logits ? fptr(gate_logits) : nullptr, indices ? (int32_t *)dptr(indices) : nullptr,
+                             scores ? fptr(scores) : nullptr, n_tokens, n_embd, n_expert, n_used, n_ff_exp,
+                             router_row_stride, router_type, norm_topk_prob, "moe_ffn_batch_noalloc", &fx);
+    g.no_alloc = false;
+    return rc;
 }
 
 extern "C" size_t ds3_hip_noalloc_scratch_bytes(void) { return kScratchBytes; }

@@ -60,6 +60,9 @@ hipError_t launch_route_mark(const RouteArgs &a, uint8_t *masks, hipStream_t s);
 // and tickets (zeroed device ints, left zeroed) the kernel may also run the
 // router tail for small T; *topk_done says whether it did.
 bool router_seq_type_ok(int rtype, int K);
+// FP32 copy of E router rows (of type rtype, K weights each, rstride bytes
+// apart) as the reference's dequantised router holds them, into dst [E][K].
+hipError_t launch_router_rows(int rtype, const uint8_t *rw, uint64_t rstride, int E, int K, float *dst, hipStream_t s);
 hipError_t launch_router_seq(const float *x, int T, int K, int E, int rtype, const uint8_t *rw, uint64_t rstride,
                              float *wf32, float *logits, int64_t ldl, _Float16 *x16, const RouteArgs *topk,
                              int *tickets, bool *topk_done, hipStream_t s);

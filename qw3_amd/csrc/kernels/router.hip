@@ -774,14 +774,8 @@ hipError_t launch_router_cert(const float *x, int T, int K, int E, int rtype, co
                                    T <= 4 ? min(13, 106496 / rowb) : min(4, 33792 / rowb), &cs);
     if (e != hipSuccess) return e;
     if ((const float *)rw != cs.w && (phases & 1)) {
-        const dim3 grid((unsigned)((K + 255) / 256), (unsigned)E);
-        switch (rtype) {
-        case T_F32: hipLaunchKernelGGL(k_router_rows_f32<T_F32>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
-        case T_F16: hipLaunchKernelGGL(k_router_rows_f32<T_F16>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
-        case T_Q8_0: hipLaunchKernelGGL(k_router_rows_f32<T_Q8_0>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
-        case T_Q4_K: hipLaunchKernelGGL(k_router_rows_f32<T_Q4_K>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
-        default: hipLaunchKernelGGL(k_router_rows_f32<T_Q6_K>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
-        }
+        e = launch_router_rows(rtype, rw, rstride, E, K, wf32, s);
+        if (e != hipSuccess) return e;
     }
     const float *w = cs.w;
     const int64_t wstride = cs.wstride;
@@ -829,6 +823,20 @@ bool router_seq_type_ok(int rtype, int K)
     return (rtype == T_Q4_K || rtype == T_Q6_K) && K % 256 == 0;
 }
 
+hipError_t launch_router_rows(int rtype, const uint8_t *rw, uint64_t rstride, int E, int K, float *dst, hipStream_t s)
+{
+    if (E <= 0 || !router_seq_type_ok(rtype, K) || dst == nullptr) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((K + 255) / 256), (unsigned)E);
+    switch (rtype) {
+    case T_F32: hipLaunchKernelGGL(k_router_rows_f32<T_F32>, grid, dim3(256), 0, s, rw, rstride, E, K, dst); break;
+    case T_F16: hipLaunchKernelGGL(k_router_rows_f32<T_F16>, grid, dim3(256), 0, s, rw, rstride, E, K, dst); break;
+    case T_Q8_0: hipLaunchKernelGGL(k_router_rows_f32<T_Q8_0>, grid, dim3(256), 0, s, rw, rstride, E, K, dst); break;
+    case T_Q4_K: hipLaunchKernelGGL(k_router_rows_f32<T_Q4_K>, grid, dim3(256), 0, s, rw, rstride, E, K, dst); break;
+    default: hipLaunchKernelGGL(k_router_rows_f32<T_Q6_K>, grid, dim3(256), 0, s, rw, rstride, E, K, dst); break;
+    }
+    return hipGetLastError();
+}
+
 template <int DW, int D>
 static void seq_launch(const float *x, int T, int K, int E, const float *w, int64_t wstride, float *logits,
                        int64_t ldl, _Float16 *x16, hipStream_t s)
@@ -850,14 +858,8 @@ hipError_t launch_router_seq(const float *x, int T, int K, int E, int rtype, con
     if (!f32_direct) {
         // FP32 copy of the rows as the reference's dequantised router holds them
         if (wf32 == nullptr) return hipErrorInvalidValue;
-        const dim3 grid((unsigned)((K + 255) / 256), (unsigned)E);
-        switch (rtype) {
-        case T_F32: hipLaunchKernelGGL(k_router_rows_f32<T_F32>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
-        case T_F16: hipLaunchKernelGGL(k_router_rows_f32<T_F16>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
-        case T_Q8_0: hipLaunchKernelGGL(k_router_rows_f32<T_Q8_0>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
-        case T_Q4_K: hipLaunchKernelGGL(k_router_rows_f32<T_Q4_K>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
-        default: hipLaunchKernelGGL(k_router_rows_f32<T_Q6_K>, grid, dim3(256), 0, s, rw, rstride, E, K, wf32); break;
-        }
+        const hipError_t er = launch_router_rows(rtype, rw, rstride, E, K, wf32, s);
+        if (er != hipSuccess) return er;
         w = wf32;
         wstride = K;
     }

@@ -70,6 +70,25 @@ class Buffer:
         b.write(a)
         return b
 
+    @classmethod
+    def from_mmap_array(cls, a: np.ndarray) -> "Buffer":
+        """A read-only device copy of a's bytes, imported the way the engine
+        imports its mmap'd GGUF weights (ds3_hip_buffer_from_mmap, from a
+        page-aligned anonymous mapping): writes to it are refused, and a
+        non-F32 router held in it is expanded to FP32 once, not per call."""
+        import mmap
+        a = np.ascontiguousarray(a)
+        n = max(a.nbytes, 1)
+        mm = mmap.mmap(-1, n)
+        try:
+            host = np.frombuffer(mm, dtype=np.uint8, count=n)
+            host[:a.nbytes] = a.reshape(-1).view(np.uint8)
+            h = hip().ds3_hip_buffer_from_mmap(host.ctypes.data, n)
+            del host
+        finally:
+            mm.close()
+        return cls(h, n)
+
     def view(self, offset: int, nbytes: int) -> "Buffer":
         return Buffer(hip().ds3_hip_buffer_view(self.handle, offset, nbytes), nbytes, owner=True)
 

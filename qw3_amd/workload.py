@@ -82,14 +82,16 @@ class HostLayer:
     down: np.ndarray                    # raw bytes [n_expert*n_embd][n_ff]
     bias: np.ndarray | None = None
 
-    def to_device(self) -> "DeviceLayer":
+    def to_device(self, readonly: bool = False) -> "DeviceLayer":
+        """readonly: import every tensor as the engine imports mmap'd GGUF
+        weights (ds3_hip_buffer_from_mmap); otherwise plain device buffers."""
         s = self.spec
+        put = ds3.Buffer.from_mmap_array if readonly else ds3.Buffer.from_array
         return DeviceLayer(
             spec=s,
-            router=ds3.Buffer.from_array(self.router),
-            experts=ds3.ExpertTensors(ds3.Buffer.from_array(self.gate), ds3.Buffer.from_array(self.up),
-                                      ds3.Buffer.from_array(self.down), s.gate_type, s.up_type, s.down_type,
-                                      s.n_embd, s.n_ff))
+            router=put(self.router),
+            experts=ds3.ExpertTensors(put(self.gate), put(self.up), put(self.down), s.gate_type, s.up_type,
+                                      s.down_type, s.n_embd, s.n_ff))
 
 
 @dataclass

@@ -13,6 +13,7 @@ import _oracle as O
 from _cases import Case, assert_close, cert_bound, index_mismatches
 from qw3_amd import ds3
 from qw3_amd import workload as W
+from qw3_amd._native import hip
 
 pytestmark = pytest.mark.gpu
 
@@ -1066,3 +1067,61 @@ def test_graph_replay(hip_ready, real, T):
             assert np.array_equal(oo.read(np.float32, (T, s.n_embd)), want_o)
     finally:
         gr.close()
+
+
+# ---------------------------------------------------------------------------
+# read-only routers: the FP32 copy made once
+# ---------------------------------------------------------------------------
+
+def _batch_run(dev, spec, x, n_used=8):
+    T = x.shape[0]
+    out = ds3.Buffer.alloc(T * spec.n_embd * 4)
+    idx = ds3.Buffer.alloc(T * n_used * 4)
+    sc = ds3.Buffer.alloc(T * n_used * 4)
+    lg = ds3.Buffer.alloc(T * spec.n_expert * 4)
+    hip().ds3_hip_kernel_timing_reset()
+    hip().ds3_hip_kernel_timing(1)
+    ds3.moe_ffn_batch(ds3.Buffer.from_array(x), dev.router, spec.router_type, dev.experts, out, T, spec.n_expert,
+                      n_used, logits=lg, indices=idx, scores=sc)
+    hip().ds3_hip_kernel_timing(0)
+    ran = set(ds3.kernel_stats())
+    return (out.read(np.float32, (T, spec.n_embd)), idx.read(np.int32, (T, n_used)), sc.read(np.float32, (T, n_used)),
+            lg.read(np.float32, (T, spec.n_expert))), ran
+
+
+def test_readonly_router_expanded_once(hip_ready):
+    """A Q8_0 router imported read-only (ds3_hip_buffer_from_mmap, as the
+    engine imports its mmap'd weights) is expanded to FP32 rows on its first
+    call only; later calls read that copy.  Results are bit-equal to a
+    writable import of the same bytes on the decode (T=1), certified batch
+    (T=4) and grouped (T=64) paths.  Freeing the buffer drops the copy: a
+    different router imported next, perhaps at the same address, routes by
+    its own rows (oracle)."""
+    spec = W.LayerSpec(ds3.TYPE_Q8_0, ds3.TYPE_Q8_0, ds3.TYPE_Q8_0, ds3.TYPE_Q8_0, n_embd=1024, n_ff=256,
+                       n_expert=32)
+    host = W.make_layer(spec, seed=4242)
+    rw, ro = host.to_device(), host.to_device(readonly=True)
+    one = np.zeros(1, np.uint8)
+    assert hip().ds3_hip_buffer_write(ro.router, 0, one.ctypes.data, 1) == -1      # read-only
+    for i, T in enumerate((1, 4, 64)):
+        x = W.fill(W.NORMAL, 30 + T, T, T * spec.n_embd, 0.0, 1.0).reshape(T, spec.n_embd)
+        print(f"  read-only Q8_0 router T={T}", flush=True)
+        want, _ = _batch_run(rw, spec, x)
+        got, ran = _batch_run(ro, spec, x)
+        assert ("router_rows" in ran) == (i == 0)        # the copy is made by the first call only
+        for a, b in zip(got, want):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    # a second router, imported after the first is freed
+    host2 = W.make_layer(spec, seed=4343)
+    ro.router.close()
+    ro2 = ds3.Buffer.from_mmap_array(host2.router)
+    case2 = Case(spec, host=host2)
+    x = W.fill(W.NORMAL, 99, 4, 4 * spec.n_embd, 0.0, 1.0).reshape(4, spec.n_embd)
+    dev2 = W.DeviceLayer(spec=spec, router=ro2, experts=ro.experts)
+    (got, gi, gs, _), ran = _batch_run(dev2, spec, x)
+    assert "router_rows" in ran
+    c1 = Case(spec, host=host)                           # the experts dev2 still uses
+    case2.wg, case2.wu, case2.wd = c1.wg, c1.wu, c1.wd
+    want, oi, osc, probs = case2.oracle(x)
+    assert index_mismatches(gi, oi, probs) == 0
+    assert_close(got, want)
