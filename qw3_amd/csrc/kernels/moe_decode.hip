@@ -24,7 +24,7 @@ static_assert(DEC_TPB == XC_THREADS, "the exact-weights stage runs on a decode w
 #endif
 constexpr int N_XCD_DEC = 8;   // MI355X: workgroups go round-robin to 8 XCDs
 #ifndef DS3_DOWN_LDS
-#define DS3_DOWN_LDS 1         // Q6_K down rows staged through LDS by DMA
+#define DS3_DOWN_LDS 1         // Q6_K / Q8_0 down rows staged through LDS by DMA
 #endif
 #ifndef DS3_SEL_RPW
 #define DS3_SEL_RPW 4          // rows per lane group in the fused-selection gate/up kernel
@@ -246,16 +246,16 @@ k_decode_down(const float *__restrict__ h, const int32_t *__restrict__ idx, cons
 }
 
 // ---------------------------------------------------------------------------
-// Q6_K down with the weights staged through LDS.  Same work split and the
-// same arithmetic as k_decode_down<Q6_K, 8, UPL> (so the same results, bit
-// for bit): wave k of the workgroup is slot k, lane group (8 lanes) per row,
-// 8 rows per wave, UPL = F / 256 units per lane.  The wave's 8 rows are
-// contiguous (8 x 210 UPL bytes, a multiple of 16) and arrive by 16-byte
-// global_load_lds DMAs together with the slot's h row, so a lane's unit
-// fields (8-byte runs at 2-byte offsets: three dword reads and two funnel
-// shifts each) and its h come from LDS instead of ~40 small global loads.
-// N % 8 == 0, F % 256 == 0 with F <= 1024, rows packed (stride 210 UPL),
-// 16-byte aligned expert bases and h.
+// Q6_K and Q8_0 down with the weights staged through LDS.  Same work split
+// and the same arithmetic as k_decode_down<DT, 8, UPL> (so the same results,
+// bit for bit): wave k of the workgroup is slot k, lane group (8 lanes) per
+// row, 8 rows per wave, UPL = F / 256 units of 32 weights per lane.  The
+// wave's 8 rows are contiguous (8 x 210 UPL or 8 x 272 UPL bytes, a multiple
+// of 16) and arrive by 16-byte global_load_lds DMAs together with the slot's
+// h row, so a lane's unit fields (runs at 2-byte offsets: dword reads and
+// funnel shifts) and its h come from LDS instead of ~20-40 small global
+// loads.  N % 8 == 0, F % 256 == 0 with F <= 1024, rows packed, 16-byte
+// aligned expert bases and h.
 // ---------------------------------------------------------------------------
 #define DS3_LDSP __attribute__((address_space(3)))
 
@@ -301,13 +301,41 @@ __device__ __forceinline__ float unit_dot_q6k_lds(uint32_t row, int u, uint32_t 
     return d * acc;
 }
 
-template <int UPL>
+__device__ __forceinline__ uint32_t lds_u32_a2(uint32_t a)
+{
+    const DS3_LDSP uint32_t *q = (const DS3_LDSP uint32_t *)(uintptr_t)(a & ~3u);
+    return __builtin_amdgcn_alignbyte(q[1], q[0], a & 3u);
+}
+
+// unit_dot_q80 with the row's block and x in LDS (byte addresses): the same
+// operations in the same order
+__device__ __forceinline__ float unit_dot_q80_lds(uint32_t row, int u, uint32_t xa)
+{
+    const uint32_t blk = row + (uint32_t)u * 34u;
+    const float d = h2f(*(const DS3_LDSP uint16_t *)(uintptr_t)blk);
+    const DS3_LDSP float *xb = (const DS3_LDSP float *)(uintptr_t)xa + 32 * u;
+    float dc = 0.f, sx = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t q = lds_u32_a2(blk + 2 + 4 * i) ^ 0x80808080u;   // int8 + 128
+        dc += dot4(q, xb + 4 * i);
+        sx += sum4(xb + 4 * i);
+    }
+    return d * (dc - 128.f * sx);
+}
+
+// Bytes of one down row of F = 256 UPL weights.
+template <int DT> struct DownRow;
+template <> struct DownRow<T_Q6_K> { static constexpr int PER256 = 210; };
+template <> struct DownRow<T_Q8_0> { static constexpr int PER256 = 272; };
+
+template <int DT, int UPL>
 __global__ void __launch_bounds__(1024)
-k_decode_down_q6k(const float *__restrict__ h, const int32_t *__restrict__ idx, const float *__restrict__ wts,
+k_decode_down_lds(const float *__restrict__ h, const int32_t *__restrict__ idx, const float *__restrict__ wts,
                   int n_used, ExpertWeights ew, int N, int F, float *__restrict__ out, int64_t ldo,
                   const float *__restrict__ residual, int accumulate)
 {
-    constexpr int G = 8, RPW = WAVE / G, ROWB = 210 * UPL;
+    constexpr int G = 8, RPW = WAVE / G, ROWB = DownRow<DT>::PER256 * UPL;
     constexpr int WB = RPW * ROWB, REGION = WB + 1024 * UPL;   // 8 rows, then h (F = 256 UPL floats)
     extern __shared__ __attribute__((aligned(16))) uint8_t dsm[];
     const int t = blockIdx.y;
@@ -335,7 +363,10 @@ k_decode_down_q6k(const float *__restrict__ h, const int32_t *__restrict__ idx, 
     const uint32_t row = reg + (uint32_t)(grp * ROWB);
     float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < UPL; i++) acc += unit_dot_q6k_lds(row, gl + G * i, reg + WB);
+    for (int i = 0; i < UPL; i++) {
+        if constexpr (DT == T_Q6_K) acc += unit_dot_q6k_lds(row, gl + G * i, reg + WB);
+        else acc += unit_dot_q80_lds(row, gl + G * i, reg + WB);
+    }
     acc = group_sum<G>(acc);
     float *part = (float *)(dsm + n_used * REGION);        // [n_used][RPW]
     if (gl == 0) part[k * RPW + grp] = acc;
@@ -474,19 +505,31 @@ hipError_t launch_decode_down(const float *h, const int32_t *idx, const float *w
 {
     if (!gemv_type_ok(ew.down_type, F) || T <= 0 || N <= 0 || n_used <= 0 || n_used > 16)
         return hipErrorInvalidValue;
-    if (DS3_DOWN_LDS && ew.down_type == T_Q6_K && N % 8 == 0 && F % 256 == 0 && F <= 1024 &&
-        ew.down_stride == (uint64_t)(210 * (F / 256)) && ((uintptr_t)ew.down & 15) == 0 &&
+    const int per256 = ew.down_type == T_Q6_K ? 210 : 272;
+    if (DS3_DOWN_LDS && (ew.down_type == T_Q6_K || ew.down_type == T_Q8_0) && N % 8 == 0 && F % 256 == 0 &&
+        F <= 1024 && ew.down_stride == (uint64_t)(per256 * (F / 256)) && ((uintptr_t)ew.down & 15) == 0 &&
         (ew.table == nullptr) && ((uintptr_t)h & 15) == 0) {
         const int upl = F / 256;
-        const size_t lds = (size_t)n_used * (8 * 210 * upl + 1024 * upl) + (size_t)n_used * 8 * sizeof(float);
+        const size_t lds = (size_t)n_used * (8 * per256 * upl + 1024 * upl) + (size_t)n_used * 8 * sizeof(float);
         const dim3 grid((unsigned)(N / 8), (unsigned)T);
-        if (lds <= 163840) switch (upl) {
-        case 1: hipLaunchKernelGGL(k_decode_down_q6k<1>, grid, dim3(n_used * WAVE), lds, s, h, idx, wts, n_used, ew, N, F, out, ldo, residual, accumulate ? 1 : 0); break;
-        case 2: hipLaunchKernelGGL(k_decode_down_q6k<2>, grid, dim3(n_used * WAVE), lds, s, h, idx, wts, n_used, ew, N, F, out, ldo, residual, accumulate ? 1 : 0); break;
-        case 3: hipLaunchKernelGGL(k_decode_down_q6k<3>, grid, dim3(n_used * WAVE), lds, s, h, idx, wts, n_used, ew, N, F, out, ldo, residual, accumulate ? 1 : 0); break;
-        default: hipLaunchKernelGGL(k_decode_down_q6k<4>, grid, dim3(n_used * WAVE), lds, s, h, idx, wts, n_used, ew, N, F, out, ldo, residual, accumulate ? 1 : 0); break;
+#define DS3_DLDS(DTV, U) hipLaunchKernelGGL((k_decode_down_lds<DTV, U>), grid, dim3(n_used * WAVE), lds, s, h, idx, \
+                                           wts, n_used, ew, N, F, out, ldo, residual, accumulate ? 1 : 0)
+        if (lds <= 163840) {
+            if (ew.down_type == T_Q6_K) switch (upl) {
+            case 1: DS3_DLDS(T_Q6_K, 1); break;
+            case 2: DS3_DLDS(T_Q6_K, 2); break;
+            case 3: DS3_DLDS(T_Q6_K, 3); break;
+            default: DS3_DLDS(T_Q6_K, 4); break;
+            }
+            else switch (upl) {
+            case 1: DS3_DLDS(T_Q8_0, 1); break;
+            case 2: DS3_DLDS(T_Q8_0, 2); break;
+            case 3: DS3_DLDS(T_Q8_0, 3); break;
+            default: DS3_DLDS(T_Q8_0, 4); break;
+            }
+            return hipGetLastError();
         }
-        if (lds <= 163840) return hipGetLastError();
+#undef DS3_DLDS
     }
     const int G = lanes_per_row(F / 32), UPL = F / 32 / G;
     const int rpw = WAVE / G;                   // one row per lane group
