@@ -8,6 +8,7 @@
 //            with y_k[j] = h[slot_k] . Wd_{e_k}[j], summed in top-k order
 //            (reference src/ds3_reference.c:674-678), no atomics.
 #include "route_select.h"
+#include "rowstream.h"
 
 namespace ds3k {
 
@@ -25,6 +26,9 @@ static_assert(DEC_TPB == XC_THREADS, "the exact-weights stage runs on a decode w
 constexpr int N_XCD_DEC = 8;   // MI355X: workgroups go round-robin to 8 XCDs
 #ifndef DS3_DOWN_LDS
 #define DS3_DOWN_LDS 1         // Q6_K / Q8_0 down rows staged through LDS by DMA
+#endif
+#ifndef DS3_GU_CHUNKED
+#define DS3_GU_CHUNKED 1       // T = 2..16 gate/up rows through the chunked row stream
 #endif
 #ifndef DS3_SEL_RPW
 #define DS3_SEL_RPW 4          // rows per lane group in the fused-selection gate/up kernel
@@ -98,6 +102,159 @@ k_decode_gate_up(const float *__restrict__ x, int64_t ldx, const int32_t *__rest
     const int r = blockIdx.x - n_exact, slot = r / nx;
     gate_up_rows<GT, G, UPL, PAIR>(x + (int64_t)(slot / n_used) * ldx, slot, r - slot * nx, idx[slot], ew, K, F,
                                    which, h);
+}
+
+// ---------------------------------------------------------------------------
+// Chunked gate/up rows (T = 2..16 decode, dense Q4_K / Q6_K / Q8_0 rows of
+// K = 2048 / 4096 from 16-byte aligned expert bases): workgroup w of slot s
+// takes chunks c = w, w + wps, ... of DG_R consecutive gate rows and the same
+// up rows, each a contiguous byte range, loaded by every thread into register
+// sets (two chunks of both matrices in flight, rowstream.h) and staged in two
+// LDS buffers; each wave dots DG_R / 4 rows of both with the slot's token x,
+// held in registers for the workgroup's whole walk, and lane 63 writes
+// h = silu(gate) * up.  Against gate_up_rows: x is read once per workgroup,
+// not once per row, and the weights arrive as whole lines.  The first
+// n_exact workgroups run the exact-weights stage as in k_decode_gate_up; both
+// paths carve the same dynamic LDS.
+// ---------------------------------------------------------------------------
+#ifndef DS3_DG_ROWS
+#define DS3_DG_ROWS 8
+#endif
+#ifndef DS3_DG_WPC
+#define DS3_DG_WPC 2
+#endif
+constexpr int DG_R = DS3_DG_ROWS;                // rows per chunk, of gate and of up
+constexpr int DG_WPC = DS3_DG_WPC;               // workgroups per CU over all slots
+
+template <int GT, int UPL>
+struct DgChunk {
+    static constexpr int RB = G1Row<GT>::RB * UPL;
+    static constexpr int CB = DG_R * RB;
+    static constexpr int NL = (CB + G1_LOAD - 1) / G1_LOAD;
+    static constexpr int BUF = NL * G1_LOAD;
+    static constexpr size_t LDS = (size_t)4 * BUF;   // two chunks of gate and up
+    static_assert(3 * NL <= 63, "three sets in flight behind the oldest");
+};
+
+template <int GT, int UPL>
+__global__ void __launch_bounds__(DEC_TPB)
+k_decode_gate_up_chunked(const float *__restrict__ x, int64_t ldx, const int32_t *__restrict__ idx, int n_used,
+                         ExpertWeights ew, int F, float *__restrict__ h, int wps, int nch, int n_exact, ExactTail xt)
+{
+    static_assert(DEC_TPB == G1_TPB, "row streaming assumes 256 threads");
+    extern __shared__ __attribute__((aligned(16))) uint8_t dl[];
+    constexpr int K = 2048 * UPL;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    if ((int)blockIdx.x < n_exact) {
+        const int t = blockIdx.x;
+        float4 xv[4];
+        exact_load_x(x + (int64_t)t * ldx, K, xv, threadIdx.x);
+        const int e_lane = lane < n_used ? idx[t * n_used + lane] : 0;
+        exact_store_x((float *)dl, K, xv, threadIdx.x);
+        __syncthreads();                                         // the row is in LDS
+        exact_weights_wg((float *)dl, K, xt.w, xt.wstride, xt.ra, t, e_lane, wave, lane);
+        return;
+    }
+    using P = DgChunk<GT, UPL>;
+    const int r = (int)blockIdx.x - n_exact, slot = r / wps;
+    int c = r - slot * wps;
+    if (c >= nch) return;                                        // uniform over the workgroup
+    const int e = idx[slot];
+    const uint8_t *wg = expert_base(ew.gate, ew.table, e, 0, (uint64_t)F, ew.gate_stride);
+    const uint8_t *wu = expert_base(ew.up, ew.table, e, 1, (uint64_t)F, ew.up_stride);
+    const int64_t lim = (int64_t)F * P::RB - 16;
+    G1Set<P::NL> SG[2], SU[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int64_t o = (int64_t)min(c + j * wps, nch - 1) * P::CB;
+        SG[j].issue(wg, o, P::CB, lim);
+        SU[j].issue(wu, o, P::CB, lim);
+    }
+    // x after the first chunks: the wait for x (vmcnt 0, in issue order)
+    // then covers them too, one memory latency instead of two
+    float xr[UPL][32], sx[UPL][4];
+    g1_load_x<GT, UPL>(x + (int64_t)(slot / n_used) * ldx, lane, xr, sx);
+    bool more = true;
+    for (int k = 0; more; k += 2) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            if (more) {                                          // uniform over the workgroup
+                SG[j].template wait<3 * P::NL>();                // SU[j] and the other chunk's pair went out after
+                SU[j].template wait<2 * P::NL>();
+                uint8_t *buf = dl + ((k + j) & 1) * 2 * P::BUF;
+                SG[j].to_lds(buf);
+                SU[j].to_lds(buf + P::BUF);
+                __syncthreads();                                 // every wave is done with this buffer's last chunk
+                const int64_t o = (int64_t)min(c + 2 * wps, nch - 1) * P::CB;
+                SG[j].issue(wg, o, P::CB, lim);
+                SU[j].issue(wu, o, P::CB, lim);
+#pragma unroll 1
+                for (int i = 0; i < DG_R / 4; i++) {
+                    const int rr = wave + 4 * i;
+                    float ag = 0.f, au = 0.f;
+#pragma unroll
+                    for (int q = 0; q < UPL; q++) {
+                        ag += g1_unit_dot<GT>(buf + rr * P::RB, lane + 64 * q, xr[q], sx[q]);
+                        au += g1_unit_dot<GT>(buf + P::BUF + rr * P::RB, lane + 64 * q, xr[q], sx[q]);
+                    }
+                    ag = g1_wave_total(ag);
+                    au = g1_wave_total(au);
+                    const int row = c * DG_R + rr;
+                    if (lane == WAVE - 1 && row < F) h[(int64_t)slot * F + row] = swiglu(ag, au);
+                }
+                c += wps;
+                more = c < nch;
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {                                // loads still in flight, registers named
+        SG[j].template wait<0>();
+        SU[j].template wait<0>();
+    }
+}
+
+template <int GT, int UPL>
+static hipError_t gate_up_chunked_t(const float *x, int64_t ldx, const int32_t *idx, int n_slots, int n_used,
+                                    const ExpertWeights &ew, int F, float *h, int n_exact, const ExactTail &tail,
+                                    size_t exact_lds, hipStream_t s)
+{
+    static int n_cu = 0;
+    if (n_cu == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+            n_cu = 256;
+    }
+    using P = DgChunk<GT, UPL>;
+    const int nch = (F + DG_R - 1) / DG_R;
+    // DG_WPC workgroups per CU over all slots, at least one per slot
+    int wps = DG_WPC * n_cu / n_slots;
+    wps = wps < 1 ? 1 : wps > nch ? nch : wps;
+    const size_t lds = std::max(P::LDS, exact_lds);
+    const dim3 grid((unsigned)(n_exact + (int64_t)wps * n_slots));
+    hipLaunchKernelGGL((k_decode_gate_up_chunked<GT, UPL>), grid, dim3(DEC_TPB), lds, s, x, ldx, idx, n_used, ew, F,
+                       h, wps, nch, n_exact, tail);
+    return hipGetLastError();
+}
+
+// The chunked kernel's shapes: gate and up of one type among Q4_K / Q6_K /
+// Q8_0, K = 2048 or 4096, dense rows, 16-byte aligned tensors, no offset
+// table (its expert offsets are on the device, where their alignment is not
+// checked).
+static bool gate_up_chunked_ok(const ExpertWeights &ew, int K)
+{
+    if (ew.gate_type != ew.up_type || (K != 2048 && K != 4096) || ew.table != nullptr) return false;
+    if (((uintptr_t)ew.gate & 15) != 0 || ((uintptr_t)ew.up & 15) != 0) return false;
+    int rb;
+    switch (ew.gate_type) {
+    case T_Q4_K: rb = G1Row<T_Q4_K>::RB; break;
+    case T_Q6_K: rb = G1Row<T_Q6_K>::RB; break;
+    case T_Q8_0: rb = G1Row<T_Q8_0>::RB; break;
+    default: return false;
+    }
+    const uint64_t row = (uint64_t)rb * (uint64_t)(K / 2048);
+    return ew.gate_stride == row && ew.up_stride == row;
 }
 
 // The exact-weights stage on its own, one workgroup per token: token t's
@@ -440,6 +597,21 @@ static hipError_t decode_gate_up_impl(const float *x, int64_t ldx, const int32_t
         return hipErrorInvalidValue;
     const ExactTail tail = xt != nullptr ? *xt : ExactTail{};
     const size_t lds = xt != nullptr ? exact_chain_lds(K) : 0;
+    if (pair && DS3_GU_CHUNKED && gate_up_chunked_ok(ew, K)) {
+        const int n_exact = xt != nullptr ? xt->ra.T : 0;
+        const bool two = K == 4096;
+        switch (ew.gate_type) {
+        case T_Q4_K:
+            return two ? gate_up_chunked_t<T_Q4_K, 2>(x, ldx, idx, n_slots, n_used, ew, F, h, n_exact, tail, lds, s)
+                       : gate_up_chunked_t<T_Q4_K, 1>(x, ldx, idx, n_slots, n_used, ew, F, h, n_exact, tail, lds, s);
+        case T_Q6_K:
+            return two ? gate_up_chunked_t<T_Q6_K, 2>(x, ldx, idx, n_slots, n_used, ew, F, h, n_exact, tail, lds, s)
+                       : gate_up_chunked_t<T_Q6_K, 1>(x, ldx, idx, n_slots, n_used, ew, F, h, n_exact, tail, lds, s);
+        default:
+            return two ? gate_up_chunked_t<T_Q8_0, 2>(x, ldx, idx, n_slots, n_used, ew, F, h, n_exact, tail, lds, s)
+                       : gate_up_chunked_t<T_Q8_0, 1>(x, ldx, idx, n_slots, n_used, ew, F, h, n_exact, tail, lds, s);
+        }
+    }
     const int G = lanes_per_row(K / 32), UPL = K / 32 / G;
     const int rows_per_wg = (DEC_TPB / WAVE) * (WAVE / G) * 2;     // 2 rows per lane group
     const int nx = (F + rows_per_wg - 1) / rows_per_wg, n_exact = xt != nullptr ? xt->ra.T : 0;
