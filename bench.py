@@ -42,7 +42,7 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
 FP16_PEAK_TFLOPS = 2500.0      # dense fp16 MFMA
-C5_TOKENS = (1, 4, 8, 16, 64, 256, 1024)
+C5_TOKENS = (1, 4, 8, 16, 32, 64, 256, 1024)
 
 
 def log(*a):
