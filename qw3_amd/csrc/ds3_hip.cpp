@@ -39,7 +39,7 @@ static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace {
 
-constexpr int kDefaultPrefillMin = 16;
+constexpr int kDefaultPrefillMin = 17;     // grouped path from this many tokens (decode kernels up to 16)
 constexpr int kDefaultDenseMfmaMin = 64;   // matmul_quantized_batch: fp16 MFMA path from this many rows of A
 constexpr int kTickets = 32;             // router token-group tickets (zero between launches)
 constexpr int kCertMaxTokens = 16;       // automatic mode: certified router up to this many tokens
