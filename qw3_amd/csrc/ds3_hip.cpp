@@ -1415,7 +1415,7 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
         o_rg = bp.take((size_t)max_tiles * rpi_gu * 4);
         o_rd = bp.take((size_t)max_tiles * rpi_dn * 4);
         o_h16 = bp.take(S * n_ff_exp * 2);
-        o_y = bp.take(S * n_embd * 4);
+        o_y = bp.take(S * n_embd * 2);
         if (mark) o_mask = bp.take((T + 3) / 4 * n_expert);
     } else {
         o_h = bp.take(T * n_used * n_ff_exp * 4);
@@ -1486,7 +1486,7 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
                   (int32_t *)(ws + o_pos), (int32_t *)(ws + o_tiles), (int32_t *)(ws + o_nt), max_tiles, 64,
                   (int32_t *)(ws + o_rg), (int32_t *)(ws + o_rd), (int32_t *)(ws + o_nt) + 1, rpi_gu, rpi_dn };
     _Float16 *x16_all = (_Float16 *)(ws + o_x16), *h16 = (_Float16 *)(ws + o_h16);
-    float *y = (float *)(ws + o_y);
+    _Float16 *y = (_Float16 *)(ws + o_y);
     if (!x16_done) {
         KScope ks("to_f16");
         const hipError_t e = launch_to_f16(x, x16_all, (int64_t)T * n_embd, g.stream);

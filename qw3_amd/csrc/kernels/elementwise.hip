@@ -110,12 +110,13 @@ __global__ void k_to_f32(const _Float16 *x, float *y, int64_t n)
 // out[t][j] = (acc ? out[t][j] : 0) + w_0 y[p_0][j] + ... in k order, then + residual.
 // Four consecutive columns per thread when N % 4 == 0 (VEC = 4), else one.
 template <int VEC>
-__global__ void k_combine(const float *__restrict__ y, const int32_t *__restrict__ slot_pos,
+__global__ void k_combine(const _Float16 *__restrict__ y, const int32_t *__restrict__ slot_pos,
                           const float *__restrict__ wts, int k, int N, float *__restrict__ out, int64_t ldo,
                           const float *__restrict__ residual, int accumulate)
 {
 #pragma clang fp contract(off)
     typedef float vec_t __attribute__((ext_vector_type(VEC)));
+    typedef _Float16 hvec_t __attribute__((ext_vector_type(VEC)));
     const int t = blockIdx.y;
     const int j = (blockIdx.x * EW_TPB + threadIdx.x) * VEC;
     if (j >= N) return;
@@ -130,7 +131,8 @@ __global__ void k_combine(const float *__restrict__ y, const int32_t *__restrict
         for (int kk = 0; kk < KMAX; kk++) {
             p[kk] = k0 + kk < k ? slot_pos[t * k + k0 + kk] : -1;
             w[kk] = p[kk] >= 0 ? wts[t * k + k0 + kk] : 0.0f;
-            v[kk] = p[kk] >= 0 ? *(const vec_t *)(y + (int64_t)p[kk] * N + j) : (vec_t)0.0f;
+            v[kk] = p[kk] >= 0 ? __builtin_convertvector(*(const hvec_t *)(y + (int64_t)p[kk] * N + j), vec_t)
+                               : (vec_t)0.0f;
         }
 #pragma unroll
         for (int kk = 0; kk < KMAX; kk++)
@@ -252,7 +254,7 @@ hipError_t launch_to_f32(const _Float16 *x, float *y, int64_t n, hipStream_t s)
     return hipGetLastError();
 }
 
-hipError_t launch_combine(const float *y, const int32_t *slot_pos, const float *wts, int T, int k, int N, float *out,
+hipError_t launch_combine(const _Float16 *y, const int32_t *slot_pos, const float *wts, int T, int k, int N, float *out,
                           int64_t ldo, const float *residual, bool accumulate, hipStream_t s)
 {
     const bool vec4 = N % 4 == 0 && ldo % 4 == 0 &&

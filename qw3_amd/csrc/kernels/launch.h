@@ -189,7 +189,7 @@ hipError_t launch_to_f32(const _Float16 *x, float *y, int64_t n, hipStream_t s);
 hipError_t launch_grouped_gate_up(const _Float16 *x16, int K, const ExpertWeights &ew, int F,
                                   const BucketOut &b, _Float16 *h16, hipStream_t s);
 hipError_t launch_grouped_down(const _Float16 *h16, int F, const ExpertWeights &ew, int N,
-                               const BucketOut &b, float *y, hipStream_t s);
+                               const BucketOut &b, _Float16 *y, hipStream_t s);
 bool grouped_type_ok(int type, int K);
 // Layer shapes the grouped kernels take: n_embd a multiple of 256 x gate_up's
 // weight ring depth (512 as built: whole activation chunks and ring turns per
@@ -211,7 +211,7 @@ hipError_t launch_dense_mfma(const _Float16 *x16, int K, const uint8_t *w, uint6
                              const BucketOut &b, float *c, hipStream_t s);
 
 // out[t][j] = (accumulate ? out : 0) + sum_k w[t][k] * y[slot_pos[t*k+kk]][j] (+ residual)
-hipError_t launch_combine(const float *y, const int32_t *slot_pos, const float *wts, int T, int k,
+hipError_t launch_combine(const _Float16 *y, const int32_t *slot_pos, const float *wts, int T, int k,
                           int N, float *out, int64_t ldo, const float *residual, bool accumulate,
                           hipStream_t s);
 

@@ -5,7 +5,7 @@
 // metal/matmul_q4k.metal:247-286) with two MFMA kernels over the bucketed
 // token lists:
 //   gate_up: H[pos][r] = silu(X_e . Wg_e[r]) * (X_e . Wu_e[r])   (fp16 out)
-//   down:    Y[pos][j] = H_e[pos] . Wd_e[j]                       (fp32 out)
+//   down:    Y[pos][j] = H_e[pos] . Wd_e[j]                       (fp16 out)
 // where pos runs over expert e's compacted token positions.
 //
 // Precision: operands are fp16 (x, dequantised weights, h), accumulation is
@@ -649,10 +649,10 @@ struct GgEpiGateUp {
     }
 };
 
-// down epilogue: y rows in fp32 (each store instruction writes 4 rows x 16
-// consecutive columns).
+// down epilogue: y rows in fp16, rounded once from the fp32 accumulators
+// (each store instruction writes 4 rows x 16 consecutive columns).
 struct GgEpiDown {
-    float *y;
+    _Float16 *y;
     int N, row0, mrows, nt0, wave, lane;
     template <int MB>
     __device__ __forceinline__ void store(const floatx4 (&acc)[MB][1], int t) const
@@ -664,7 +664,7 @@ struct GgEpiDown {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int mr = 16 * mb + 4 * g + j;
-                if (mr < mrows) y[(int64_t)(row0 + mr) * N + col] = acc[mb][0][j];
+                if (mr < mrows) y[(int64_t)(row0 + mr) * N + col] = (_Float16)acc[mb][0][j];
             }
     }
 };
@@ -815,7 +815,7 @@ k_grouped_gate_up(const _Float16 *__restrict__ x16, int K, ExpertWeights ew, int
 template <int TYPE>
 __global__ void __launch_bounds__(64 * GG_WV)
 k_grouped_down(const _Float16 *__restrict__ h16, int F, ExpertWeights ew, int N, BucketOut b,
-               float *__restrict__ y, int ntb)
+               _Float16 *__restrict__ y, int ntb)
 {
     __shared__ __attribute__((aligned(16))) uint8_t smem[GG_DN_LDS];
     const int n_nt = N / GG_TILE_N;
@@ -915,8 +915,8 @@ static hipError_t gate_up_t(const _Float16 *x16, int K, const ExpertWeights &ew,
 }
 
 template <int TV>
-static hipError_t down_t(const _Float16 *h16, int F, const ExpertWeights &ew, int N, const BucketOut &b, float *y,
-                         hipStream_t s)
+static hipError_t down_t(const _Float16 *h16, int F, const ExpertWeights &ew, int N, const BucketOut &b,
+                         _Float16 *y, hipStream_t s)
 {
     const unsigned grid = gg_grid(b.max_tiles * b.rpi_dn);
     hipLaunchKernelGGL((k_grouped_down<TV>), dim3(grid), dim3(64 * GG_WV), 0, s, h16, F, ew, N, b, y,
@@ -983,7 +983,7 @@ hipError_t launch_dense_mfma(const _Float16 *x16, int K, const uint8_t *w, uint6
 }
 
 hipError_t launch_grouped_down(const _Float16 *h16, int F, const ExpertWeights &ew, int N, const BucketOut &b,
-                               float *y, hipStream_t s)
+                               _Float16 *y, hipStream_t s)
 {
     int rg, rd;
     grouped_runs_per_tile(N, F, rg, rd);
