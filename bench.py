@@ -98,7 +98,7 @@ def kernel_bytes(name, spec, T, counts, n_used):
     exact = S * K * 4 if T <= 16 else 0
     return {
         "moe_grouped_gate_up": distinct * gu + T * K * 2 + S * F * 2,
-        "moe_grouped_down": distinct * dn + S * F * 2 + S * K * 4,
+        "moe_grouped_down": distinct * dn + S * F * 2 + S * K * 2,      # y in fp16
         "moe_decode_gate_up": distinct * gu + T * K * 4 + S * F * 4 + exact,
         # with the certified selection in its prologue: also reads S and B
         "moe_decode_gate_up_sel": distinct * gu + T * K * 4 + S * F * 4 + T * E * (8 + 4) + exact,
