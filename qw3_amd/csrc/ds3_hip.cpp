@@ -740,23 +740,22 @@ extern "C" int ds3_hip_matmul_quantized_batch(const ds3_hip_buffer_t *A, const d
         // fp16 MFMA path: A in fp16, the weights decoded to fp16, fp32
         // accumulate, on the grouped gate_up kernel as one expert that holds
         // every row of A (the bucketing lists of M zero expert indices)
-        const int rpi_gu = dense_runs_per_tile((int)N), rpi_dn = 1;   // down's list is written, not used
+        const int rpi_gu = dense_runs_per_tile((int)N);         // gate_up's run list only: no down
         const int max_tiles = (int)((M + 63) / 64) + 1;
         Bump bp;
-        const size_t o_x16 = bp.take((size_t)M * K * 2), o_idx = bp.take((size_t)M * 4), o_cnt = bp.take(16),
-                     o_off = bp.take(16), o_ids = bp.take((size_t)M * 4), o_wts = bp.take((size_t)M * 4),
-                     o_pos = bp.take((size_t)M * 4), o_tiles = bp.take((size_t)max_tiles * 4), o_nt = bp.take(16),
-                     o_rg = bp.take((size_t)max_tiles * rpi_gu * 4), o_rd = bp.take((size_t)max_tiles * rpi_dn * 4);
+        const size_t o_x16 = bp.take((size_t)M * K * 2), o_cnt = bp.take(16), o_off = bp.take(16),
+                     o_ids = bp.take((size_t)M * 4), o_wts = bp.take((size_t)M * 4), o_pos = bp.take((size_t)M * 4),
+                     o_tiles = bp.take((size_t)max_tiles * 4), o_nt = bp.take(16),
+                     o_rg = bp.take((size_t)max_tiles * rpi_gu * 4);
         uint8_t *ws = ws_get(bp.off);
         if (!ws) return -1;
         BucketOut bo{ (int32_t *)(ws + o_cnt), (int32_t *)(ws + o_off), (int32_t *)(ws + o_ids), (float *)(ws + o_wts),
                       (int32_t *)(ws + o_pos), (int32_t *)(ws + o_tiles), (int32_t *)(ws + o_nt), max_tiles, 64,
-                      (int32_t *)(ws + o_rg), (int32_t *)(ws + o_rd), (int32_t *)(ws + o_nt) + 1, rpi_gu, rpi_dn };
-        hipError_t e = launch_fill_zero((float *)(ws + o_idx), M, g.stream);      // expert 0 for every row
-        if (e == hipSuccess) e = launch_to_f16(fptr(A), (_Float16 *)(ws + o_x16), (int64_t)M * K, g.stream);
+                      (int32_t *)(ws + o_rg), nullptr, (int32_t *)(ws + o_nt) + 1, rpi_gu, 0 };
+        hipError_t e = launch_to_f16(fptr(A), (_Float16 *)(ws + o_x16), (int64_t)M * K, g.stream);
         if (e == hipSuccess) {
             KScope ks("dense_lists");
-            e = launch_bucket((const int32_t *)(ws + o_idx), (const float *)(ws + o_idx), (int)M, 1, 1, bo, g.stream);
+            e = launch_dense_lists((int)M, bo, g.stream);           // one expert holding every row, in order
         }
         if (e == hipSuccess) {
             KScope ks("dense_mfma");

@@ -356,6 +356,42 @@ hipError_t launch_bucket_place(const int32_t *idx, const float *scores, const ui
     return hipGetLastError();
 }
 
+// The lists of a dense product (matmul_quantized_batch on the grouped
+// kernel): one expert holding rows 0 .. M-1 in order with weight 1, work
+// items 0 .. nt-1, and the run lists in item order -- which is k_bucket's
+// heaviest-first order here, as every tile but the last is full.
+__global__ void __launch_bounds__(BUCKET_TPB) k_dense_lists(int M, BucketOut o)
+{
+    const int nt = (M + o.tile_m - 1) / o.tile_m;
+    for (int i = threadIdx.x; i < M; i += BUCKET_TPB) {
+        o.ids[i] = i;
+        o.wts[i] = 1.0f;
+        o.slot_pos[i] = i;
+    }
+    for (int q = threadIdx.x; q < nt; q += BUCKET_TPB) o.tiles[q] = q;      // expert 0, tile q
+    for (int i = threadIdx.x; i < nt * o.rpi_gu; i += BUCKET_TPB) o.runs_gu[i] = ((i / o.rpi_gu) << 12) | (i % o.rpi_gu);
+    if (o.runs_dn != nullptr)
+        for (int i = threadIdx.x; i < nt * o.rpi_dn; i += BUCKET_TPB)
+            o.runs_dn[i] = ((i / o.rpi_dn) << 12) | (i % o.rpi_dn);
+    if (threadIdx.x == 0) {
+        o.counts[0] = M;
+        o.offsets[0] = 0;
+        o.offsets[1] = M;
+        *o.n_tiles = nt;
+        o.n_runs[0] = nt * o.rpi_gu;
+        o.n_runs[1] = o.runs_dn != nullptr ? nt * o.rpi_dn : 0;
+    }
+}
+
+hipError_t launch_dense_lists(int M, const BucketOut &o, hipStream_t s)
+{
+    if (M <= 0 || o.tile_m <= 0 || o.runs_gu == nullptr || o.rpi_gu <= 0 || (M + o.tile_m - 1) / o.tile_m > o.max_tiles ||
+        (M + o.tile_m - 1) / o.tile_m > 4095)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_dense_lists, dim3(1), dim3(BUCKET_TPB), 0, s, M, o);
+    return hipGetLastError();
+}
+
 hipError_t launch_bucket(const int32_t *idx, const float *scores, int T, int k, int E, const BucketOut &o,
                          hipStream_t s)
 {

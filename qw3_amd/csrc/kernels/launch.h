@@ -180,6 +180,8 @@ hipError_t launch_bucket(const int32_t *idx, const float *scores, int T, int k, 
 // The same lists from launch_route_mark's bitmaps (the rows of these T
 // tokens), one workgroup per 32 tokens.  T <= 2048, k <= 32, E <= 256,
 // max_tiles <= 1280.
+// The lists of a dense product: one expert holding rows 0 .. M-1, in order.
+hipError_t launch_dense_lists(int M, const BucketOut &o, hipStream_t s);
 hipError_t launch_bucket_place(const int32_t *idx, const float *scores, const uint8_t *masks, int T, int k, int E,
                                const BucketOut &o, hipStream_t s);
 
