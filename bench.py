@@ -103,7 +103,8 @@ def kernel_bytes(name, spec, T, counts, n_used):
         # with the certified selection in its prologue: also reads S and B
         "moe_decode_gate_up_sel": distinct * gu + T * K * 4 + S * F * 4 + T * E * (8 + 4) + exact,
         "moe_decode_down": distinct * dn + S * F * 4 + T * K * 4,
-        "router_logits": W.router_bytes(spec) + T * K * 4 + T * E * 4,
+        # on the grouped path (T > 16 by default) the router launch also writes x in fp16
+        "router_logits": W.router_bytes(spec) + T * K * 4 + T * E * 4 + (T * K * 2 if T > 16 else 0),
         # certified router: the sums read the router and x, write S, B and the logits;
         # the selection reads S and B
         "router_sums": W.router_bytes(spec) + T * K * 4 + T * E * (8 + 4 + 4),
@@ -467,13 +468,14 @@ def leg_c5(args, traffic):
     return r
 
 
-def leg_dense(args):
+def leg_dense(args, traffic):
     """The engine's dense quantised products beside the MoE (reference
     src/ds3_engine.c:181-271): the output head (2048 -> 151,936 logits, one
     token: vec_matmul, HBM-bound) in Q6_K and Q8_0, and a prefill projection
     (M = 512 rows, 2048 -> 4096, Q4_K: matmul_quantized_batch) on its fp16
     MFMA path and on its fp32 path.  Two weight copies alternate per call so
-    the head's 255-330 MB cannot stay in the 256 MB Infinity Cache."""
+    the head's 255-330 MB cannot stay in the 256 MB Infinity Cache.  The
+    head's measured traffic per launch is under "head/<type>/gemv1"."""
     from qw3_amd import ds3
     from qw3_amd import workload as W
     from qw3_amd._native import hip
@@ -512,7 +514,8 @@ def leg_dense(args):
         head[ds3.TYPE_NAMES[t]] = {
             "us_per_call": round(k_s * 1e6, 2), "wall_us_per_call": round(wall * 1e6, 2), "alg_bytes": b,
             "roofline": {"bound": "hbm", "achieved": round(b / k_s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(b / k_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "gemv1"}}
+                         "frac": round(b / k_s / 1e9 / HBM_PEAK_GBS, 4),
+                         "traffic": (traffic or {}).get(f"head/{ds3.TYPE_NAMES[t]}/gemv1"), "kernel": "gemv1"}}
         log(f"[bench] dense: head {ds3.TYPE_NAMES[t]} {k_s * 1e6:.1f} us ({b / k_s / 1e12:.2f} TB/s)")
         if t == ds3.TYPE_Q6_K and not args.no_cpu:
             sys.path.insert(0, str(ROOT / "tests"))
@@ -840,7 +843,7 @@ def main():
         if "c4" not in skip:
             line["c4"] = leg_stack(args, traffic)
         if "dense" not in skip:
-            line["dense"] = leg_dense(args)
+            line["dense"] = leg_dense(args, traffic)
     print(json.dumps(line), flush=True)
 
 
