@@ -269,6 +269,28 @@ __device__ __forceinline__ uint32_t place_mask(const uint8_t *rowsb, int c, int 
     return m;
 }
 
+// Copies n16 16-byte pieces of the bitmap rows into LDS, N per thread: all N
+// loads are issued (a load past the last piece re-reads it and is not
+// written), then the pieces are written.  N * BUCKET_TPB >= n16.
+template <int N>
+__device__ __forceinline__ void place_copy_rows(const uint8_t *__restrict__ masks, uint8_t *rowsb, int n16)
+{
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    const int i0 = threadIdx.x;
+    u32x4_t v[N];
+#pragma unroll
+    for (int u = 0; u < N; u++) v[u] = ((const u32x4_t *)masks)[min(i0 + BUCKET_TPB * u, n16 - 1)];
+    // the compiler would otherwise sink each load into its write's branch and wait there
+    if constexpr (N == 2) asm volatile("" : "+v"(v[0]), "+v"(v[1]));
+    if constexpr (N == 4) asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
+    if constexpr (N == 8)
+        asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]),
+                     "+v"(v[7]));
+#pragma unroll
+    for (int u = 0; u < N; u++)
+        if (i0 + BUCKET_TPB * u < n16) ((u32x4_t *)rowsb)[i0 + BUCKET_TPB * u] = v[u];
+}
+
 __global__ void __launch_bounds__(BUCKET_TPB)
 k_bucket_place(const int32_t *__restrict__ idx, const float *__restrict__ scores, const uint8_t *__restrict__ masks,
                int T, int k, int E, BucketOut o)
@@ -281,9 +303,17 @@ k_bucket_place(const int32_t *__restrict__ idx, const float *__restrict__ scores
     __shared__ __attribute__((aligned(16))) uint8_t rowsb[PLACE_MAX_T / 4 * PLACE_MAX_E];   // all rows of the call
     const int c = blockIdx.x, chunks = (T + 31) / 32, rows = (T + 3) / 4;
     {
-        // every row into LDS at once: 16-byte loads (masks 16-byte aligned), the tail by bytes
+        // every row into LDS at once: 16-byte loads (masks 16-byte aligned),
+        // all of a thread's loads issued before any is written, so the copy
+        // is one memory round trip; the tail by bytes
         const int nb = rows * E, n16 = nb / 16;
-        for (int i = threadIdx.x; i < n16; i += BUCKET_TPB) ((uint4 *)rowsb)[i] = ((const uint4 *)masks)[i];
+        static_assert(8 * BUCKET_TPB * 16 >= PLACE_MAX_T / 4 * PLACE_MAX_E, "8 loads per thread cover every row");
+        const int nper = (n16 + BUCKET_TPB - 1) / BUCKET_TPB;     // loads per thread, <= 8
+        if (n16 <= 0) {
+        } else if (nper == 1) place_copy_rows<1>(masks, rowsb, n16);
+        else if (nper == 2) place_copy_rows<2>(masks, rowsb, n16);
+        else if (nper <= 4) place_copy_rows<4>(masks, rowsb, n16);
+        else place_copy_rows<8>(masks, rowsb, n16);
         for (int i = 16 * n16 + (int)threadIdx.x; i < nb; i += BUCKET_TPB) rowsb[i] = masks[i];
     }
     __syncthreads();

@@ -59,7 +59,7 @@ __device__ __forceinline__ float key_float(uint32_t k)
 // Softmax + top-k + renorm of one token by one wave from its E logits at lg
 // (E <= 256); writes the k indices to oi and weights to os.  The pointers
 // may address global memory or LDS.
-__device__ inline void route_token_row(const float *lg, int E, int k, bool norm, int32_t *oi, float *os, int lane)
+__device__ inline int route_token_row(const float *lg, int E, int k, bool norm, int32_t *oi, float *os, int lane)
 {
     float l[ROUTE_EPL];
     bool finite = true;
@@ -134,7 +134,7 @@ __device__ inline void route_token_row(const float *lg, int E, int k, bool norm,
                 oi[lane] = my_e;
                 os[lane] = w;
             }
-            return;                             // uniform over the wave
+            return lane < k ? my_e : -1;        // uniform over the wave
         }
     }
 
@@ -184,12 +184,14 @@ __device__ inline void route_token_row(const float *lg, int E, int k, bool norm,
         oi[lane] = sel_i;
         os[lane] = w;
     }
+    return lane < k ? sel_i : -1;
 }
 
-// Softmax + top-k + renorm of token t of a by one wave.
-__device__ inline void route_token(const RouteArgs &a, int t, int lane)
+// Softmax + top-k + renorm of token t of a by one wave; lane r < k gets the
+// expert of rank r back (the value it stored), the other lanes -1.
+__device__ inline int route_token(const RouteArgs &a, int t, int lane)
 {
-    route_token_row(a.logits + (int64_t)t * a.logit_stride, a.E, a.k, a.norm, a.idx + (int64_t)t * a.out_stride,
+    return route_token_row(a.logits + (int64_t)t * a.logit_stride, a.E, a.k, a.norm, a.idx + (int64_t)t * a.out_stride,
                     a.scores + (int64_t)t * a.out_stride, lane);
 }
 

@@ -529,11 +529,8 @@ __global__ void __launch_bounds__(256) k_route_mark(RouteArgs a, uint8_t *__rest
     __syncthreads();
     const int t = blockIdx.x * 4 + wave;
     if (t < a.T) {                                        // uniform over the wave
-        route_token(a, t, lane);
-        if (lane < a.k) {
-            const int e = a.idx[(int64_t)t * a.out_stride + lane];   // this lane's own store
-            if (e >= 0 && e < a.E) atomicOr(&m_l[e], 1u << (t & 3));
-        }
+        const int e = route_token(a, t, lane);           // lane r < k: the expert it stored for rank r
+        if (e >= 0 && e < a.E) atomicOr(&m_l[e], 1u << (t & 3));
     }
     __syncthreads();
     for (int e = threadIdx.x; e < a.E; e += blockDim.x) masks[(int64_t)blockIdx.x * a.E + e] = (uint8_t)m_l[e];
