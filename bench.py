@@ -52,20 +52,21 @@ def log(*a):
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=1000)
+    p.add_argument("--warmup", type=int, default=100,
+                   help="untimed steps enqueued back to back right before each timed region")
     p.add_argument("--tokens", type=int, default=None, help="tokens per step of a --config 2/3/5 run")
     p.add_argument("--layers", type=int, default=8, help="distinct resident layers cycled per step")
     p.add_argument("--config", type=int, default=0, choices=(0, 2, 3, 4, 5),
                    help="0 (default): every configuration in one line; 2, 3, 5: one layer on --tokens tokens "
                         "(+ T=1 under t1 for 2); 4: the decode stack alone")
     p.add_argument("--stack-layers", type=int, default=48, help="config 4: resident layers per decode step")
-    p.add_argument("--stack-steps", type=int, default=50)
+    p.add_argument("--stack-steps", type=int, default=200)
     p.add_argument("--no-graph", action="store_true",
                    help="configs 4 and the T=1 leg: enqueue every call eagerly instead of replaying captured HIP graphs")
     p.add_argument("--stack-block", action="store_true",
                    help="config 4: run each layer as the engine's FFN block (RMSNorm + MoE + residual)")
-    p.add_argument("--t1-steps", type=int, default=208)
+    p.add_argument("--t1-steps", type=int, default=1008)
     p.add_argument("--t1-zero", action="store_true",
                    help="T=1 leg: zero the output before every call (default: each call accumulates into the "
                         "output, the decode residual stream, with no zeroing launch)")
@@ -140,35 +141,28 @@ def held(step):
     return run
 
 
+BRK_STEPS = 20                 # steps of the per-kernel breakdown pass
+
+
 def time_steps(step, steps, warmup, spec, T, n_used, first, per_kernel=True, graph_of=0):
     """`first()` runs one step and returns the routed indices [T][n_used];
-    then warmup steps with every kernel timed (breakdown, dominant kernel),
-    the timed steps with no per-kernel events, and the same steps again with
-    only the dominant kernel bracketed by events.  With graph_of = G > 0 the
-    timed steps are replays of one HIP graph of steps 0 .. G-1 (steps a
-    multiple of G), as a decode loop replays its captured calls.  Returns
-    (wall_ms, gpu_ms, stats, breakdown, counts)."""
+    then `warmup` plain untimed steps back to back (the GPU reaches its
+    sustained clocks and the layers' address translations are warm: the first
+    few milliseconds of a burst run ~10 % slower), the timed steps with no
+    per-kernel events, BRK_STEPS steps with every kernel bracketed by events
+    (the breakdown, which names the dominant kernel), and the timed steps
+    again with only the dominant kernel bracketed (its mean duration for the
+    roofline).  The two event passes follow the timed region, so they see the
+    same sustained state.  With graph_of = G > 0 the warmup and timed steps
+    are replays of one HIP graph of steps 0 .. G-1 (steps a multiple of G), as
+    a decode loop replays its captured calls.  Returns (wall_ms, gpu_ms,
+    stats, breakdown, counts)."""
     from qw3_amd import ds3
     from qw3_amd._native import hip
     E = spec.n_expert
     idx = first()
     hip().ds3_hip_synchronize()
     counts = np.bincount(idx.reshape(-1), minlength=E)
-    brk, dominant = {}, None
-    hstep = held(step) if per_kernel else step
-    if per_kernel:
-        hip().ds3_hip_kernel_timing_only(None)
-        hip().ds3_hip_kernel_timing_reset()
-        hip().ds3_hip_kernel_timing(1)
-    hip().ds3_hip_begin_batch()
-    for i in range(1, warmup + 1):
-        hstep(i)
-    hip().ds3_hip_end_batch()
-    if per_kernel:
-        hip().ds3_hip_kernel_timing(0)
-        brk = ds3.kernel_stats()
-        dominant = max((k for k in brk if kernel_bytes(k, spec, T, counts, n_used) is not None),
-                       key=lambda k: brk[k][1])
     graph = None
     if graph_of:
         assert steps % graph_of == 0
@@ -176,7 +170,15 @@ def time_steps(step, steps, warmup, spec, T, n_used, first, per_kernel=True, gra
         with graph:
             for i in range(graph_of):
                 step(i)
-        graph.launch()                          # one untimed replay
+    # warmup: plain steps (graph replays), enqueued back to back and untimed
+    hip().ds3_hip_begin_batch()
+    if graph is not None:
+        for _ in range(max(1, warmup // graph_of)):
+            graph.launch()
+    else:
+        for i in range(warmup):
+            step(i)
+    hip().ds3_hip_end_batch()
     # timed region: synchronise, K steps enqueued back to back, synchronise;
     # no per-kernel events in it (at T = 1 an event pair costs a third of a step)
     hip().ds3_hip_synchronize()
@@ -194,10 +196,22 @@ def time_steps(step, steps, warmup, spec, T, n_used, first, per_kernel=True, gra
     wall_ms = (time.perf_counter() - t0) * 1e3
     if graph is not None:
         graph.close()
-    stats = {}
+    brk, stats = {}, {}
     if per_kernel:
-        # the same steps again with only the dominant kernel bracketed by
-        # events on the library's stream: its average duration for the roofline
+        hstep = held(step)
+        # breakdown: every kernel bracketed by events on the library's stream
+        hip().ds3_hip_kernel_timing_only(None)
+        hip().ds3_hip_kernel_timing_reset()
+        hip().ds3_hip_kernel_timing(1)
+        hip().ds3_hip_begin_batch()
+        for i in range(BRK_STEPS):
+            hstep(i)
+        hip().ds3_hip_end_batch()
+        hip().ds3_hip_kernel_timing(0)
+        brk = ds3.kernel_stats()
+        dominant = max((k for k in brk if kernel_bytes(k, spec, T, counts, n_used) is not None),
+                       key=lambda k: brk[k][1])
+        # the timed steps again with only the dominant kernel bracketed
         hip().ds3_hip_kernel_timing_reset()
         hip().ds3_hip_kernel_timing_only(dominant.encode())
         hip().ds3_hip_kernel_timing(1)
@@ -259,7 +273,7 @@ def roofline(stats, spec, T, counts, n_used, traffic):
 
 
 def log_breakdown(brk, stats):
-    log("[bench]   warmup, every kernel bracketed by events:")
+    log(f"[bench]   breakdown pass ({BRK_STEPS} steps), every kernel bracketed by events:")
     for k, (n, ms) in sorted(brk.items(), key=lambda kv: -kv[1][1]):
         log(f"[bench]     {k:24s} {n:5d} launches  avg {ms / n * 1e3:8.2f} us")
     for k, (n, ms) in stats.items():
@@ -389,7 +403,7 @@ def leg_layer(args, config, T, steps, warmup, spec, layers, xs, traffic, n_used=
     flops = W.algorithmic_flops(spec, T, n_used)
     return {
         "value": round(T / (ms / 1e3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 5), "steps": steps,
-        "tokens": T, "alg_bytes_per_step": b,
+        "warmup": warmup, "tokens": T, "alg_bytes_per_step": b,
         "hbm_frac_step": round(b / (ms / 1e3) / (HBM_PEAK_GBS * 1e9), 4),
         "mfma_util": round(flops / (ms / 1e3) / (FP16_PEAK_TFLOPS * 1e12), 4),
         "roofline": roofline(stats, spec, T, counts, n_used, traffic),
@@ -410,7 +424,7 @@ def leg_c3(args, traffic):
     host, layers = make_layers(spec, 4, "c3")
     xh = [W.make_inputs(3, 2048, seed=99, step=s) for s in range(2)]
     xs = [ds3.Buffer.from_array(x) for x in xh]
-    r = leg_layer(args, 3, 2048, 10, 2, spec, layers, xs, traffic, what="c3")
+    r = leg_layer(args, 3, 2048, 100, 20, spec, layers, xs, traffic, what="c3")
     flops = W.algorithmic_flops(spec, 2048)
     r["mfma_roofline"] = {"bound": "mfma", "achieved": round(flops / (r["ms_per_step"] / 1e3) / 1e12, 1),
                           "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": r["mfma_util"],
@@ -439,9 +453,9 @@ def leg_c5(args, traffic):
         row = {}
         for path, mn in (("gemv", 1 << 30), ("grouped", 1)):
             ds3.set_prefill_min_tokens(mn)
-            steps = 50 if T <= 64 else 10
+            steps = 200 if T <= 64 else 50
             step, first = layer_steps(T, layers, xs, spec)
-            wall_ms, _, _, _, counts = time_steps(step, steps, 2, spec, T, 8, first, per_kernel=False)
+            wall_ms, _, _, _, counts = time_steps(step, steps, steps // 5, spec, T, 8, first, per_kernel=False)
             ms = wall_ms / steps
             b = W.algorithmic_bytes(spec, T, int((counts > 0).sum()))
             row[path] = {"ms_per_step": round(ms, 5), "tokens_per_s": round(T / (ms / 1e3), 1),
@@ -456,7 +470,7 @@ def leg_c5(args, traffic):
     # dominant-kernel roofline at the headline-sized T of the sweep, default path
     T = 256
     xs = [ds3.Buffer.from_array(W.make_inputs(5, T, seed=99, step=s)) for s in range(4)]
-    dom = leg_layer(args, 5, T, 10, 2, spec, layers, xs, traffic, what="c5")
+    dom = leg_layer(args, 5, T, 100, 20, spec, layers, xs, traffic, what="c5")
     faster = [int(t) for t, r in sweep.items() if r["faster"] == "grouped"]
     slower = [int(t) for t, r in sweep.items() if r["faster"] == "gemv"]
     r = {"sweep": sweep, "prefill_min_tokens": default_min,
@@ -622,22 +636,12 @@ def leg_stack(args, traffic, n_used=8):
             graph.launch()
 
     # graph replays record no per-kernel events: the breakdown and the
-    # dominant kernel's events come from eager tokens (time_steps' first and
-    # last passes use `token` through the same function)
+    # dominant kernel's events come from eager tokens after the timed region
+    # (`token`, the function the graph captured)
     steps = args.stack_steps
     idx0 = first()
     counts = np.bincount(idx0, minlength=E)
     htoken = held(token)
-    hip().ds3_hip_kernel_timing_only(None)
-    hip().ds3_hip_kernel_timing_reset()
-    hip().ds3_hip_kernel_timing(1)
-    hip().ds3_hip_begin_batch()
-    for i in range(1, 3):
-        htoken(i)
-    hip().ds3_hip_end_batch()
-    hip().ds3_hip_kernel_timing(0)
-    brk = ds3.kernel_stats()
-    dominant = max((k for k in brk if kernel_bytes(k, spec, 1, counts, n_used) is not None), key=lambda k: brk[k][1])
     hip().ds3_hip_begin_batch()
     for i in range(args.warmup):
         step(i)
@@ -649,6 +653,17 @@ def leg_stack(args, traffic, n_used=8):
         step(i)
     hip().ds3_hip_end_batch()
     wall_ms = (time.perf_counter() - t0) * 1e3
+    # the event passes after the timed region, in the same sustained state
+    hip().ds3_hip_kernel_timing_only(None)
+    hip().ds3_hip_kernel_timing_reset()
+    hip().ds3_hip_kernel_timing(1)
+    hip().ds3_hip_begin_batch()
+    for i in range(2):
+        htoken(i)
+    hip().ds3_hip_end_batch()
+    hip().ds3_hip_kernel_timing(0)
+    brk = ds3.kernel_stats()
+    dominant = max((k for k in brk if kernel_bytes(k, spec, 1, counts, n_used) is not None), key=lambda k: brk[k][1])
     hip().ds3_hip_kernel_timing_reset()
     hip().ds3_hip_kernel_timing_only(dominant.encode())
     hip().ds3_hip_kernel_timing(1)
@@ -668,7 +683,7 @@ def leg_stack(args, traffic, n_used=8):
     b = L * W.algorithmic_bytes(spec, 1, n_used)
     r = {
         "value": round(1 / (ms / 1e3), 1), "unit": "tokens/s", "ms_per_step": round(ms, 5), "steps": steps,
-        "layers": L, "alg_bytes_per_step": b, "hbm_frac_step": round(b / (ms / 1e3) / (HBM_PEAK_GBS * 1e9), 4),
+        "warmup": args.warmup, "layers": L, "alg_bytes_per_step": b, "hbm_frac_step": round(b / (ms / 1e3) / (HBM_PEAK_GBS * 1e9), 4),
         "us_per_layer": round(ms * 1e3 / L, 3), "graph": graph is not None, "stack_block": bool(args.stack_block),
         "roofline": roofline(stats, spec, 1, counts, n_used, traffic),
         "workload": f"configs[3]: decode, one token per step through {L} resident Qwen3-30B-A3B MoE-FFN layers "

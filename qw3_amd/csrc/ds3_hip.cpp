@@ -746,12 +746,13 @@ extern "C" int ds3_hip_matmul_quantized_batch(const ds3_hip_buffer_t *A, const d
         const size_t o_x16 = bp.take((size_t)M * K * 2), o_cnt = bp.take(16), o_off = bp.take(16),
                      o_ids = bp.take((size_t)M * 4), o_wts = bp.take((size_t)M * 4), o_pos = bp.take((size_t)M * 4),
                      o_tiles = bp.take((size_t)max_tiles * 4), o_nt = bp.take(16),
-                     o_rg = bp.take((size_t)max_tiles * rpi_gu * 4);
+                     o_rg = bp.take((size_t)max_tiles * rpi_gu * 4), o_dg = bp.take((size_t)max_tiles * rpi_gu * 8);
         uint8_t *ws = ws_get(bp.off);
         if (!ws) return -1;
         BucketOut bo{ (int32_t *)(ws + o_cnt), (int32_t *)(ws + o_off), (int32_t *)(ws + o_ids), (float *)(ws + o_wts),
                       (int32_t *)(ws + o_pos), (int32_t *)(ws + o_tiles), (int32_t *)(ws + o_nt), max_tiles, 64,
-                      (int32_t *)(ws + o_rg), nullptr, (int32_t *)(ws + o_nt) + 1, rpi_gu, 0 };
+                      (int32_t *)(ws + o_rg), nullptr, (int32_t *)(ws + o_nt) + 1, rpi_gu, 0, (int2 *)(ws + o_dg),
+                      nullptr };
         hipError_t e = launch_to_f16(fptr(A), (_Float16 *)(ws + o_x16), (int64_t)M * K, g.stream);
         if (e == hipSuccess) {
             KScope ks("dense_lists");
@@ -1399,7 +1400,7 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
     const RouteScratch rs = route_scratch((int)T, n_embd, n_expert);
     const size_t o_w = bp.take(rs.bytes);
     size_t o_h = 0, o_t = 0, o_x16 = 0, o_cnt = 0, o_off = 0, o_ids = 0, o_wts = 0, o_pos = 0, o_tiles = 0, o_nt = 0,
-           o_h16 = 0, o_y = 0, o_rg = 0, o_rd = 0, o_mask = 0;
+           o_h16 = 0, o_y = 0, o_rg = 0, o_rd = 0, o_dg = 0, o_dd = 0, o_mask = 0;
     int rpi_gu = 0, rpi_dn = 0;
     if (use_grouped) {
         grouped_runs_per_tile((int)n_embd, (int)n_ff_exp, rpi_gu, rpi_dn);
@@ -1413,6 +1414,8 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
         o_nt = bp.take(16);                          // n_tiles, then the two run counts
         o_rg = bp.take((size_t)max_tiles * rpi_gu * 4);
         o_rd = bp.take((size_t)max_tiles * rpi_dn * 4);
+        o_dg = bp.take((size_t)max_tiles * rpi_gu * 8);
+        o_dd = bp.take((size_t)max_tiles * rpi_dn * 8);
         o_h16 = bp.take(S * n_ff_exp * 2);
         o_y = bp.take(S * n_embd * 2);
         if (mark) o_mask = bp.take((T + 3) / 4 * n_expert);
@@ -1483,7 +1486,8 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
     }
     BucketOut bo{ (int32_t *)(ws + o_cnt), (int32_t *)(ws + o_off), (int32_t *)(ws + o_ids), (float *)(ws + o_wts),
                   (int32_t *)(ws + o_pos), (int32_t *)(ws + o_tiles), (int32_t *)(ws + o_nt), max_tiles, 64,
-                  (int32_t *)(ws + o_rg), (int32_t *)(ws + o_rd), (int32_t *)(ws + o_nt) + 1, rpi_gu, rpi_dn };
+                  (int32_t *)(ws + o_rg), (int32_t *)(ws + o_rd), (int32_t *)(ws + o_nt) + 1, rpi_gu, rpi_dn,
+                  (int2 *)(ws + o_dg), (int2 *)(ws + o_dd) };
     _Float16 *x16_all = (_Float16 *)(ws + o_x16), *h16 = (_Float16 *)(ws + o_h16);
     _Float16 *y = (_Float16 *)(ws + o_y);
     if (!x16_done) {

@@ -77,21 +77,27 @@ __host__ __device__ constexpr size_t bucket_stage_words(int chunks, int E)
 }
 
 // Work items and run lists (every thread of the block calls it, after the
-// count scan): e = threadIdx.x, cnt = expert e's slot count, tb = its first
-// tile, ntile = its tiles, total_t = all tiles; xs: LDS scratch of
-// 3E words + max_tiles halfwords.  Per-expert tile facts go to xs: each
-// tile's expert, each expert's first tile, and for the run lists the tile
-// counts by cost class.
-__device__ void bucket_lists(int e, int cnt, int tb, int ntile, int total_t, int E, const BucketOut &o, int2 *wsum,
-                             uint32_t *xs)
+// count scan): e = threadIdx.x, cnt = expert e's slot count, off = its first
+// list position, tb = its first tile, ntile = its tiles, total_t = all
+// tiles; xs: LDS scratch of BUCKET_XS_WORDS(E, max_tiles) words.  Per-expert
+// tile facts go to xs: each tile's expert, each expert's first tile, offset
+// and count, and for the run lists the tile counts by cost class.
+__host__ __device__ constexpr int bucket_xs_words(int E, int max_tiles) { return 5 * E + (max_tiles + 1) / 2; }
+
+__device__ void bucket_lists(int e, int cnt, int off, int tb, int ntile, int total_t, int E, const BucketOut &o,
+                             int2 *wsum, uint32_t *xs)
 {
     const int nt = total_t < o.max_tiles ? total_t : o.max_tiles;
     int *tb_s = (int *)xs;                        // [E] first tile of each expert
     uint32_t *info_s = xs + E;                    // [E] full tiles << 16 | m blocks of the last tile
     uint32_t *cpos_s = info_s + E;                // [E] class-4 position << 16 | last tile's class position
-    uint16_t *own_s = (uint16_t *)(cpos_s + E);   // [nt] expert of each tile
+    int *off_s = (int *)(cpos_s + E);             // [E] first list position of each expert
+    int *cnt_s = off_s + E;                       // [E] slot count of each expert
+    uint16_t *own_s = (uint16_t *)(cnt_s + E);    // [nt] expert of each tile
     if (e < E) {
         tb_s[e] = tb;
+        off_s[e] = off;
+        cnt_s[e] = cnt;
         for (int m = 0; m < ntile && tb + m < nt; m++) own_s[tb + m] = (uint16_t)e;
     }
     const bool runs = o.runs_gu != nullptr;
@@ -129,8 +135,17 @@ __device__ void bucket_lists(int e, int cnt, int tb, int ntile, int total_t, int
             const bool c4 = m < (int)(inf >> 16) || (inf & 0xffffu) == 4u;
             const int pos = c4 ? (int)(cp >> 16) + m : (int)(cp & 0xffffu);
             if (pos < o.max_tiles) {
-                for (int j = 0; j < o.rpi_gu; j++) o.runs_gu[pos * o.rpi_gu + j] = (q << 12) | j;
-                for (int j = 0; j < o.rpi_dn; j++) o.runs_dn[pos * o.rpi_dn + j] = (q << 12) | j;
+                // the run's descriptor: its tile's first list position and rows
+                const int row0 = off_s[lo] + m * o.tile_m, mrows = min(o.tile_m, cnt_s[lo] - m * o.tile_m);
+                const int dy = (lo << 16) | (mrows << 8);
+                for (int j = 0; j < o.rpi_gu; j++) {
+                    o.runs_gu[pos * o.rpi_gu + j] = (q << 12) | j;
+                    if (o.desc_gu) o.desc_gu[pos * o.rpi_gu + j] = make_int2(row0, dy | j);
+                }
+                for (int j = 0; j < o.rpi_dn; j++) {
+                    o.runs_dn[pos * o.rpi_dn + j] = (q << 12) | j;
+                    if (o.desc_dn) o.desc_dn[pos * o.rpi_dn + j] = make_int2(row0, dy | j);
+                }
             }
         }
     }
@@ -211,7 +226,7 @@ k_bucket(const int32_t *__restrict__ idx, const float *__restrict__ scores, int 
         o.offsets[E] = total;
         *o.n_tiles = total_t < o.max_tiles ? total_t : o.max_tiles;
     }
-    bucket_lists(e, cnt, tb, ntile, total_t, E, o, wsum, sm + bucket_stage_words(chunks, E));
+    bucket_lists(e, cnt, off, tb, ntile, total_t, E, o, wsum, sm + bucket_stage_words(chunks, E));
     auto place = [&](int s, int ex, float sc) {
         const int t = s / k;
         if (ex < 0 || ex >= E) {          // out-of-range id: the slot is dropped
@@ -299,7 +314,7 @@ k_bucket_place(const int32_t *__restrict__ idx, const float *__restrict__ scores
     __shared__ int32_t off_s[PLACE_MAX_E], pre_s[PLACE_MAX_E];
     __shared__ uint32_t own_s[PLACE_MAX_E];       // this chunk's bitmaps
     __shared__ int2 wsum[BUCKET_TPB / WAVE];
-    __shared__ uint32_t xs[3 * PLACE_MAX_E + (PLACE_MAX_TILES + 1) / 2];
+    __shared__ uint32_t xs[bucket_xs_words(PLACE_MAX_E, PLACE_MAX_TILES)];
     __shared__ __attribute__((aligned(16))) uint8_t rowsb[PLACE_MAX_T / 4 * PLACE_MAX_E];   // all rows of the call
     const int c = blockIdx.x, chunks = (T + 31) / 32, rows = (T + 3) / 4;
     {
@@ -356,7 +371,7 @@ k_bucket_place(const int32_t *__restrict__ idx, const float *__restrict__ scores
             o.offsets[E] = total;
             *o.n_tiles = total_t < o.max_tiles ? total_t : o.max_tiles;
         }
-        bucket_lists(e, cnt, tb, ntile, total_t, E, o, wsum, xs);   // its barriers also publish off_s, pre_s
+        bucket_lists(e, cnt, off, tb, ntile, total_t, E, o, wsum, xs);   // its barriers also publish off_s, pre_s
     } else {
         __syncthreads();
     }
@@ -399,10 +414,17 @@ __global__ void __launch_bounds__(BUCKET_TPB) k_dense_lists(int M, BucketOut o)
         o.slot_pos[i] = i;
     }
     for (int q = threadIdx.x; q < nt; q += BUCKET_TPB) o.tiles[q] = q;      // expert 0, tile q
-    for (int i = threadIdx.x; i < nt * o.rpi_gu; i += BUCKET_TPB) o.runs_gu[i] = ((i / o.rpi_gu) << 12) | (i % o.rpi_gu);
+    for (int i = threadIdx.x; i < nt * o.rpi_gu; i += BUCKET_TPB) {
+        const int q = i / o.rpi_gu, j = i % o.rpi_gu;
+        o.runs_gu[i] = (q << 12) | j;
+        if (o.desc_gu) o.desc_gu[i] = make_int2(q * o.tile_m, (min(o.tile_m, M - q * o.tile_m) << 8) | j);
+    }
     if (o.runs_dn != nullptr)
-        for (int i = threadIdx.x; i < nt * o.rpi_dn; i += BUCKET_TPB)
-            o.runs_dn[i] = ((i / o.rpi_dn) << 12) | (i % o.rpi_dn);
+        for (int i = threadIdx.x; i < nt * o.rpi_dn; i += BUCKET_TPB) {
+            const int q = i / o.rpi_dn, j = i % o.rpi_dn;
+            o.runs_dn[i] = (q << 12) | j;
+            if (o.desc_dn) o.desc_dn[i] = make_int2(q * o.tile_m, (min(o.tile_m, M - q * o.tile_m) << 8) | j);
+        }
     if (threadIdx.x == 0) {
         o.counts[0] = M;
         o.offsets[0] = 0;
@@ -430,7 +452,7 @@ hipError_t launch_bucket(const int32_t *idx, const float *scores, int T, int k, 
     if (T <= 0 || T > 65535 || k <= 0 || E <= 0 || E > 1024 || lds > BUCKET_MASK_BYTES || o.max_tiles < 0)
         return hipErrorInvalidValue;
     // the per-expert tile facts and the tile owner table share the staging area
-    if (bucket_stage_words(chunks, E) * 4 + (size_t)3 * E * 4 + (size_t)o.max_tiles * 2 > BUCKET_LDS_BYTES)
+    if ((bucket_stage_words(chunks, E) + (size_t)bucket_xs_words(E, o.max_tiles)) * 4 > BUCKET_LDS_BYTES)
         return hipErrorInvalidValue;
     const size_t staged = bucket_stage_words(chunks, E) * 4 + (size_t)T * k * (sizeof(float) + sizeof(uint16_t));
     const int stage = staged <= BUCKET_LDS_BYTES ? 1 : 0;

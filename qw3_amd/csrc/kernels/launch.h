@@ -174,6 +174,11 @@ struct BucketOut {
     int32_t *runs_dn;    // [max_tiles * rpi_dn]
     int32_t *n_runs;     // [2]: gate_up runs, down runs
     int rpi_gu, rpi_dn;  // n-runs per token tile (n tiles / n tiles per run)
+    // Optional descriptors of the same runs, entry for entry (null: not
+    // written): { first list position of the run's tile, expert << 16 |
+    // tile rows << 8 | n run }, so a grouped kernel starts a run from one load.
+    int2 *desc_gu;       // [max_tiles * rpi_gu]
+    int2 *desc_dn;       // [max_tiles * rpi_dn]
 };
 hipError_t launch_bucket(const int32_t *idx, const float *scores, int T, int k, int E,
                          const BucketOut &o, hipStream_t s);

@@ -586,21 +586,6 @@ __device__ __forceinline__ void gg_fill_a(uint32_t a_lds, int rows_alloc, int S,
             gg_dma16(src[kk] + 256 * s, a_lds + (uint32_t)s * sbytes + (uint32_t)(2 * (wave + GG_WV * kk) * GG_SLICE));
 }
 
-// Work item header: bucketing tile `item` (expert, 64-token tile).
-struct GgItem {
-    int e, off, m0, count;
-};
-__device__ __forceinline__ bool gg_item(const BucketOut &b, int item, GgItem &it)
-{
-    if (item >= *b.n_tiles) return false;
-    const int packed = b.tiles[item];
-    it.e = packed >> 16;
-    it.off = b.offsets[it.e];
-    it.m0 = (packed & 0xffff) * GG_TILE_M;
-    it.count = b.counts[it.e];
-    return true;
-}
-
 // Persistent schedule over the bucketing kernel's run list (heaviest runs
 // first): round k of the grid (gridDim.x a multiple of 8; workgroup w sits on
 // XCD w % 8) takes list entries k*G .. k*G+G-1, consecutive entries on the
@@ -774,31 +759,31 @@ k_grouped_gate_up(const _Float16 *__restrict__ x16, int K, ExpertWeights ew, int
     const uint32_t stage = a_lds + (uint32_t)(2 * GG_CHUNK + wave * GG_STAGE);
     uint32_t lofs[8];
     gg_lofs<TYPE>(lane, lofs);
-    const int n_runs = b.n_runs[0];
-    for (int k = 0;; k++) {
-        const int i = gg_list_index(k);
-        if (i >= n_runs) break;                             // uniform over the workgroup
-        const int packed = b.runs_gu[i];
-        GgItem it;
-        if (!gg_item(b, packed >> 12, it)) continue;
-        const int j = packed & 255;
-        const int mrows = min(GG_TILE_M, it.count - it.m0);
+    // the run count and the first run's descriptor in one round trip; each
+    // later descriptor is loaded while the run before it computes
+    const int n_runs = b.n_runs[0], cap = b.max_tiles * b.rpi_gu;
+    int i = gg_list_index(0);
+    int2 d = b.desc_gu[min(i, cap - 1)];
+    for (int k = 0; i < n_runs; k++) {                      // uniform over the workgroup
+        const int e = d.y >> 16, mrows = (d.y >> 8) & 255, j = d.y & 255, row0 = d.x;
         const int mblocks = (mrows + 15) / 16;
         const int nt0 = j * ntb, nnt = min(ntb, n_nt - nt0);
         // every wave's DMAs of the previous run have landed and its reads of
         // the buffers are done before this run's DMAs overwrite them
         gg_dma_done();
-        const int32_t *ids = b.ids + it.off + it.m0;
-        const uint8_t *wg = gg_ebase(ew.gate, ew.table, it.e, 0, (uint64_t)F, ew.gate_stride);
-        const uint8_t *wu = gg_ebase(ew.up, ew.table, it.e, 1, (uint64_t)F, ew.up_stride);
+        i = gg_list_index(k + 1);
+        d = b.desc_gu[min(i, cap - 1)];
+        const int32_t *ids = b.ids + row0;
+        const uint8_t *wg = gg_ebase(ew.gate, ew.table, e, 0, (uint64_t)F, ew.gate_stride);
+        const uint8_t *wu = gg_ebase(ew.up, ew.table, e, 1, (uint64_t)F, ew.up_stride);
         const size_t r0 = (size_t)nt0 * GG_TILE_N + 16 * wave + (lane & 15);
         const uint8_t *const rows[2] = { wg + r0 * ew.gate_stride, wu + r0 * ew.up_stride };
         const uint64_t tstride = (uint64_t)GG_TILE_N * ew.gate_stride;    // gate and up strides are equal
         const bool al = gg_aligned<TYPE>(wg, wu, ew.gate_stride);
         using Epi = std::conditional_t<PLAIN, GgEpiPlain, GgEpiGateUp>;
         Epi epi;
-        if constexpr (PLAIN) epi = GgEpiPlain{ c, 2 * F, F, it.off + it.m0, mrows, nt0, wave, lane };
-        else epi = GgEpiGateUp{ h16, F, it.off + it.m0, mrows, nt0, wave, lane, stage };
+        if constexpr (PLAIN) epi = GgEpiPlain{ c, 2 * F, F, row0, mrows, nt0, wave, lane };
+        else epi = GgEpiGateUp{ h16, F, row0, mrows, nt0, wave, lane, stage };
 #define DS3_GU_CASE(MBV)                                                                                      \
     if (al) gg_gate_up_run<TYPE, true, MBV>(x16, K, ids, mrows, rows, tstride, nnt, a_lds, lofs, wave, lane, epi); \
     else gg_gate_up_run<TYPE, false, MBV>(x16, K, ids, mrows, rows, tstride, nnt, a_lds, lofs, wave, lane, epi);
@@ -825,19 +810,16 @@ k_grouped_down(const _Float16 *__restrict__ h16, int F, ExpertWeights ew, int N,
     const uint32_t step_bytes = (uint32_t)(GG_TILE_M * GG_SLICE);
     uint32_t lofs[8];
     gg_lofs<TYPE>(lane, lofs);
-    const int n_runs = b.n_runs[1];
-    for (int k = 0;; k++) {
-        const int i = gg_list_index(k);
-        if (i >= n_runs) break;                             // uniform over the workgroup
-        const int packed = b.runs_dn[i];
-        GgItem it;
-        if (!gg_item(b, packed >> 12, it)) continue;
-        const int run = packed & 255;
-        const int mrows = min(GG_TILE_M, it.count - it.m0);
+    // the run count and the first run's descriptor in one round trip; each
+    // later descriptor is loaded while the run before it computes
+    const int n_runs = b.n_runs[1], cap = b.max_tiles * b.rpi_dn;
+    int i = gg_list_index(0);
+    int2 d = b.desc_dn[min(i, cap - 1)];
+    for (int k = 0; i < n_runs; k++) {                      // uniform over the workgroup
+        const int e = d.y >> 16, mrows = (d.y >> 8) & 255, run = d.y & 255, row0 = d.x;
         const int mblocks = (mrows + 15) / 16;
         const int nt0 = run * ntb, nnt = min(ntb, n_nt - nt0);
         gg_barrier();
-        const int row0 = it.off + it.m0;
         auto src_row = [&](int r) { return h16 + (int64_t)(row0 + r) * F; };
         switch (mblocks) {
         case 1: gg_fill_a<1>(a_lds, GG_TILE_M, S, mrows, wave, lane, src_row); break;
@@ -845,11 +827,13 @@ k_grouped_down(const _Float16 *__restrict__ h16, int F, ExpertWeights ew, int N,
         case 3: gg_fill_a<3>(a_lds, GG_TILE_M, S, mrows, wave, lane, src_row); break;
         default: gg_fill_a<4>(a_lds, GG_TILE_M, S, mrows, wave, lane, src_row); break;
         }
-        const uint8_t *wd = gg_ebase(ew.down, ew.table, it.e, 2, (uint64_t)N, ew.down_stride);
+        const uint8_t *wd = gg_ebase(ew.down, ew.table, e, 2, (uint64_t)N, ew.down_stride);
         const uint8_t *const rows[1] = { wd + ((size_t)nt0 * GG_TILE_N + 16 * wave + (lane & 15)) * ew.down_stride };
         const uint64_t tstride = (uint64_t)GG_TILE_N * ew.down_stride;
         const GgEpiDown epi{ y, N, row0, mrows, nt0, wave, lane };
         gg_dma_done();
+        i = gg_list_index(k + 1);
+        d = b.desc_dn[min(i, cap - 1)];
         if (gg_aligned<TYPE>(wd, wd, ew.down_stride))
             gg_run_mb<TYPE, true, 1, DS3_GG_DEPTH>(mblocks, rows, tstride, S, nnt, a_lds, step_bytes, lofs, g, epi);
         else
@@ -930,7 +914,8 @@ hipError_t launch_grouped_gate_up(const _Float16 *x16, int K, const ExpertWeight
     int rg, rd;
     grouped_runs_per_tile(K, F, rg, rd);
     if (ew.gate_type != ew.up_type || ew.gate_stride != ew.up_stride || !grouped_type_ok(ew.gate_type, K) ||
-        b.tile_m != GG_TILE_M || !grouped_shape_ok(K, F) || b.runs_gu == nullptr || b.rpi_gu != rg)
+        b.tile_m != GG_TILE_M || !grouped_shape_ok(K, F) || b.runs_gu == nullptr || b.desc_gu == nullptr ||
+        b.rpi_gu != rg || b.max_tiles < 1)
         return hipErrorInvalidValue;
     switch (ew.gate_type) {
     case T_Q4_K: return gate_up_t<T_Q4_K>(x16, K, ew, F, b, h16, s);
@@ -964,7 +949,8 @@ hipError_t launch_dense_mfma(const _Float16 *x16, int K, const uint8_t *w, uint6
 {
     const int rg = dense_runs_per_tile(N);
     const uint64_t row_b = type == T_Q8_0 ? (uint64_t)(K / 32) * 34 : (uint64_t)(K / 256) * (type == T_Q4_K ? 144 : 210);
-    if (!dense_mfma_shape_ok(type, N, K) || b.tile_m != GG_TILE_M || b.runs_gu == nullptr || b.rpi_gu != rg ||
+    if (!dense_mfma_shape_ok(type, N, K) || b.tile_m != GG_TILE_M || b.runs_gu == nullptr || b.desc_gu == nullptr ||
+        b.rpi_gu != rg || b.max_tiles < 1 ||
         stride < row_b)
         return hipErrorInvalidValue;
     ExpertWeights ew{};
@@ -988,7 +974,7 @@ hipError_t launch_grouped_down(const _Float16 *h16, int F, const ExpertWeights &
     int rg, rd;
     grouped_runs_per_tile(N, F, rg, rd);
     if (!grouped_type_ok(ew.down_type, F) || b.tile_m != GG_TILE_M || !grouped_shape_ok(N, F) ||
-        b.runs_dn == nullptr || b.rpi_dn != rd)
+        b.runs_dn == nullptr || b.desc_dn == nullptr || b.rpi_dn != rd || b.max_tiles < 1)
         return hipErrorInvalidValue;
     switch (ew.down_type) {
     case T_Q4_K: return down_t<T_Q4_K>(h16, F, ew, N, b, y, s);
