@@ -332,6 +332,14 @@ int ds3_hip_router_stats(uint64_t *certified, uint64_t *repaired, int reset);
 int ds3_hip_debug_grouped_lists(int32_t *meta, int32_t *counts, int32_t *offsets, int32_t *ids, float *wts,
                                 int32_t *slot_pos, int32_t *tiles, int32_t *runs_gu, int32_t *runs_dn);
 
+/* No ds3_metal.h counterpart (a test hook, like ds3_hip_debug_grouped_lists):
+ * the run descriptors the grouped kernels start each run from, entry for
+ * entry with that call's runs_gu / runs_dn (their counts are meta[5] and
+ * meta[6] there): two int32 per run, { first list position of the run's work
+ * item, expert << 16 | the work item's rows << 8 | n run }.  Synchronises;
+ * -1 when no grouped call ran since the workspace last moved. */
+int ds3_hip_debug_grouped_descs(int32_t *desc_gu, int32_t *desc_dn);
+
 /* No ds3_metal.h counterpart: the row count of A from which
  * ds3_hip_matmul_quantized_batch takes its fp16 MFMA path (see there).  0
  * restores the default (64).  Returns the previous value. */

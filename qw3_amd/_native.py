@@ -76,6 +76,7 @@ SIGNATURES: dict[str, tuple] = {
     "ds3_hip_set_router_mode": (C.c_int, [C.c_int]),
     "ds3_hip_router_stats": (C.c_int, [C.POINTER(U64), C.POINTER(U64), C.c_int]),
     "ds3_hip_debug_grouped_lists": (C.c_int, [P, P, P, P, P, P, P, P, P]),
+    "ds3_hip_debug_grouped_descs": (C.c_int, [P, P]),
     "ds3_hip_set_dense_mfma_min_rows": (C.c_int, [C.c_int]),
     "ds3_hip_set_prefill_min_tokens": (C.c_int, [C.c_int]),
     "ds3_hip_kernel_timing": (None, [C.c_int]),

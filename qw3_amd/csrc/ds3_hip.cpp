@@ -1680,6 +1680,25 @@ extern "C" int ds3_hip_debug_grouped_lists(int32_t *meta, int32_t *counts, int32
     return 0;
 }
 
+extern "C" int ds3_hip_debug_grouped_descs(int32_t *desc_gu, int32_t *desc_dn)
+{
+    if (refuse_in_capture("debug_grouped_descs") || !ensure_init()) return -1;
+    if (!g.lists.valid || g.lists.bo.desc_gu == nullptr || g.lists.bo.desc_dn == nullptr) {
+        fprintf(stderr, "ds3_hip: debug_grouped_descs: no grouped-path call since the workspace last moved\n");
+        return -1;
+    }
+    const BucketOut &o = g.lists.bo;
+    int32_t n[2] = { 0, 0 };
+    if (hipStreamSynchronize(g.stream) != hipSuccess ||
+        hipMemcpy(n, o.n_runs, 8, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    if (desc_gu && n[0] > 0 && hipMemcpy(desc_gu, o.desc_gu, (size_t)n[0] * 8, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    if (desc_dn && n[1] > 0 && hipMemcpy(desc_dn, o.desc_dn, (size_t)n[1] * 8, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    return 0;
+}
+
 extern "C" int ds3_hip_router_stats(uint64_t *certified, uint64_t *repaired, int reset)
 {
     if (refuse_in_capture("router_stats") || !ensure_init()) return -1;

@@ -273,7 +273,8 @@ def router_stats(reset: bool = False) -> tuple[int, int]:
 
 def grouped_lists() -> dict:
     """The bucketing lists of the last chunk of the last grouped-path call
-    (ds3_hip_debug_grouped_lists), as numpy arrays."""
+    (ds3_hip_debug_grouped_lists) and its run descriptors
+    (ds3_hip_debug_grouped_descs), as numpy arrays."""
     h = hip()
     meta = np.zeros(12, np.int32)
     _check(h.ds3_hip_debug_grouped_lists(meta.ctypes.data, *([None] * 8)), "debug_grouped_lists")
@@ -284,6 +285,9 @@ def grouped_lists() -> dict:
          "runs_gu": np.zeros(ngu, np.int32), "runs_dn": np.zeros(ndn, np.int32)}
     _check(h.ds3_hip_debug_grouped_lists(meta.ctypes.data, *(v.ctypes.data for v in a.values())),
            "debug_grouped_lists")
+    dg, dd = np.zeros((ngu, 2), np.int32), np.zeros((ndn, 2), np.int32)
+    _check(h.ds3_hip_debug_grouped_descs(dg.ctypes.data, dd.ctypes.data), "debug_grouped_descs")
+    a.update(desc_gu=dg, desc_dn=dd)
     a.update(t0=t0, tc=tc, k=k, E=E, marked=bool(marked), rpi_gu=rpi_gu, rpi_dn=rpi_dn, max_tiles=max_tiles,
              tile_m=tile_m)
     return a

@@ -313,9 +313,9 @@ def check_lists(L: dict, idx: np.ndarray, sc: np.ndarray):
     oracle's bucketing of the same routing (reference src/ds3_engine.c:932-955:
     counts, offsets, token ids and weights in token order per expert, the
     position of every slot), bit for bit; then its work items (every expert's
-    tiles of tile_m positions in expert order) and run lists (every work item
+    tiles of tile_m positions in expert order), run lists (every work item
     once per n run, heaviest first: items of 4 m blocks of 16 tokens, then 3,
-    2, 1, each class in item order)."""
+    2, 1, each class in item order) and the runs' descriptors."""
     E, k, tile_m = L["E"], L["k"], L["tile_m"]
     t0, tc = L["t0"], L["tc"]
     ci, cs = idx[t0:t0 + tc], sc[t0:t0 + tc]
@@ -332,9 +332,17 @@ def check_lists(L: dict, idx: np.ndarray, sc: np.ndarray):
         e, m = q >> 16, q & 0xFFFF
         mb.append((min(tile_m, int(oc[e]) - m * tile_m) + 15) // 16)
     order = [q for c in (4, 3, 2, 1) for q in range(len(want_tiles)) if mb[q] == c]
-    for runs, rpi in ((L["runs_gu"], L["rpi_gu"]), (L["runs_dn"], L["rpi_dn"])):
+    for runs, rpi, desc in ((L["runs_gu"], L["rpi_gu"], L["desc_gu"]), (L["runs_dn"], L["rpi_dn"], L["desc_dn"])):
         want_runs = [(q << 12) | j for q in order for j in range(rpi)]
         assert runs.tolist() == want_runs
+        # each run's descriptor: its work item's first list position, then
+        # expert << 16 | the item's rows << 8 | n run
+        want_desc = []
+        for q in order:
+            e, m = want_tiles[q] >> 16, want_tiles[q] & 0xFFFF
+            rows = min(tile_m, int(oc[e]) - m * tile_m)
+            want_desc += [[int(oo[e]) + m * tile_m, (e << 16) | (rows << 8) | j] for j in range(rpi)]
+        assert desc.tolist() == want_desc
 
 
 @pytest.mark.parametrize("E,k,T", [(128, 8, 37), (128, 8, 512), (128, 8, 2048), (128, 8, 2050), (48, 8, 300),
