@@ -1,8 +1,8 @@
 """The allocation-free entry point ds3_hip_moe_ffn_batch_noalloc against
 ds3_hip_moe_ffn_batch, through the C ABI: identical outputs, indices, scores
 and logits on consecutive calls (the second smaller, so it runs on what the
-first left in the shared scratch array), and a clear refusal of a call whose
-intermediates exceed the scratch array."""
+first left in the shared scratch array), a clear refusal of a call whose
+intermediates exceed the scratch array, and the documented capacity edge."""
 import numpy as np
 import pytest
 
@@ -63,3 +63,26 @@ def test_noalloc_refuses_oversized_call(hip_ready, layer, capfd):
     xs = ds3.Buffer.from_array(W.make_inputs(2, 16, seed=800))
     got, want = _run(layer, xs, 16, True), _run(layer, xs, 16, False)
     assert all(np.array_equal(g, w) for g, w in zip(got, want))
+
+
+def test_noalloc_capacity_edge(hip_ready, layer):
+    """The documented capacity for a Qwen3-30B-A3B layer call: 1,285 tokens
+    fit the scratch array (and match the allocating entry point), 1,286 are
+    refused."""
+    s = layer.spec
+    T = 1285
+    print(f"  noalloc at its capacity, T={T}", flush=True)
+    x = ds3.Buffer.from_array(W.make_inputs(2, T, seed=900))
+    got, want = _run(layer, x, T, True), _run(layer, x, T, False)
+    assert all(np.array_equal(g, w) for g, w in zip(got, want))
+    T = 1286
+    print(f"  noalloc one token past it, T={T}", flush=True)
+    x = ds3.Buffer.alloc(T * s.n_embd * 4)
+    out = ds3.Buffer.alloc(T * s.n_embd * 4)
+    ex = layer.dev.experts
+    gs, us, dsd = ex.strides
+    rc = hip().ds3_hip_moe_ffn_batch_noalloc(
+        x, layer.dev.router, ex.gate, ex.up, ex.down, ex.gate_type, ex.up_type, ex.down_type, gs, us, dsd, None,
+        out, None, None, None, None, T, s.n_embd, s.n_expert, W.N_USED, s.n_ff,
+        ds3.row_bytes(s.router_type, s.n_embd), s.router_type, True)
+    assert rc == -1
