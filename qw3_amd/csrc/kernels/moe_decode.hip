@@ -21,7 +21,9 @@ __device__ __forceinline__ const uint8_t *expert_base(const uint8_t *base, const
 constexpr int DEC_TPB = 256;
 static_assert(DEC_TPB == XC_THREADS, "the exact-weights stage runs on a decode workgroup's four waves");
 #ifndef DS3_DOWN_PREFETCH
+#ifndef DS3_DOWN_PREFETCH
 #define DS3_DOWN_PREFETCH 1    // T = 1: the fused gate/up kernel warms L2 with the down rows
+#endif
 #endif
 constexpr int N_XCD_DEC = 8;   // MI355X: workgroups go round-robin to 8 XCDs
 #ifndef DS3_DOWN_LDS
