@@ -108,8 +108,7 @@ __global__ void k_to_f32(const _Float16 *x, float *y, int64_t n)
 }
 
 // out[t][j] = (acc ? out[t][j] : 0) + w_0 y[p_0][j] + ... in k order, then + residual.
-// VEC consecutive columns per thread: 8 (16-byte y loads) when N % 8 == 0, 4
-// when N % 4 == 0, else one.
+// VEC consecutive columns per thread: 8 (16-byte y loads) or one.
 template <int VEC>
 __global__ void k_combine(const _Float16 *__restrict__ y, const int32_t *__restrict__ slot_pos,
                           const float *__restrict__ wts, int k, int N, float *__restrict__ out, int64_t ldo,
@@ -122,6 +121,7 @@ __global__ void k_combine(const _Float16 *__restrict__ y, const int32_t *__restr
     const int j = (blockIdx.x * EW_TPB + threadIdx.x) * VEC;
     if (j >= N) return;
     constexpr int KMAX = VEC == 8 ? 8 : 16;   // slots whose loads are issued together
+    static_assert(VEC == 8 || VEC == 1, "8 columns per thread or one");
     float *o = out + (int64_t)t * ldo + j;
     vec_t acc = accumulate ? *(const vec_t *)o : (vec_t)0.0f;
     for (int k0 = 0; k0 < k; k0 += KMAX) {
@@ -258,15 +258,13 @@ hipError_t launch_to_f32(const _Float16 *x, float *y, int64_t n, hipStream_t s)
 hipError_t launch_combine(const _Float16 *y, const int32_t *slot_pos, const float *wts, int T, int k, int N, float *out,
                           int64_t ldo, const float *residual, bool accumulate, hipStream_t s)
 {
-    const bool vec4 = N % 4 == 0 && ldo % 4 == 0 &&
+    // 8 columns per thread (16-byte y loads) whenever the rows allow it (the
+    // grouped path's n_embd is a multiple of 128); one otherwise
+    const bool vec8 = N % 8 == 0 && ldo % 4 == 0 &&
                       ((((uintptr_t)y) | ((uintptr_t)out) | ((uintptr_t)residual)) & 15) == 0;
-    if (vec4 && N % 8 == 0) {
+    if (vec8) {
         const dim3 grid((unsigned)((N / 8 + EW_TPB - 1) / EW_TPB), (unsigned)T);
         hipLaunchKernelGGL(k_combine<8>, grid, dim3(EW_TPB), 0, s, y, slot_pos, wts, k, N, out, ldo, residual,
-                           accumulate ? 1 : 0);
-    } else if (vec4) {
-        const dim3 grid((unsigned)((N / 4 + EW_TPB - 1) / EW_TPB), (unsigned)T);
-        hipLaunchKernelGGL(k_combine<4>, grid, dim3(EW_TPB), 0, s, y, slot_pos, wts, k, N, out, ldo, residual,
                            accumulate ? 1 : 0);
     } else {
         const dim3 grid((unsigned)((N + EW_TPB - 1) / EW_TPB), (unsigned)T);

@@ -1133,3 +1133,32 @@ def test_readonly_router_expanded_once(hip_ready):
     want, oi, osc, probs = case2.oracle(x)
     assert index_mismatches(gi, oi, probs) == 0
     assert_close(got, want)
+
+
+def test_grouped_combine_unaligned_output(hip_ready):
+    """The grouped path into output and residual rows that are not 16-byte
+    aligned (views 4 bytes into their buffers): the combine then adds one
+    column per thread instead of eight, with the same operations in the same
+    order per column, so the result is the aligned call's, bit for bit."""
+    spec = W.LayerSpec(n_embd=1024, n_ff=256, n_expert=128)
+    case = Case(spec, seed=733)
+    T, K = 100, spec.n_embd
+    x = ds3.Buffer.from_array(W.fill(W.NORMAL, 19, T, T * K, 0.0, 1.0).reshape(T, K))
+    base = np.full((T, K), 0.5, np.float32)
+    resid = W.fill(W.NORMAL, 20, T, T * K, 0.0, 1.0).reshape(T, K)
+    print(f"  grouped combine into unaligned rows, T={T}", flush=True)
+    outs = []
+    for off in (0, 4):
+        ob = ds3.Buffer.alloc(T * K * 4 + 16)
+        rb = ds3.Buffer.alloc(T * K * 4 + 16)
+        out, res = ob.view(off, T * K * 4), rb.view(off, T * K * 4)
+        out.write(base)
+        res.write(resid)
+        ds3.set_prefill_min_tokens(1)
+        try:
+            ds3.moe_ffn_batch(x, case.dev.router, spec.router_type, case.dev.experts, out, T, spec.n_expert,
+                              W.N_USED, residual=res)
+        finally:
+            ds3.set_prefill_min_tokens(0)
+        outs.append(out.read(np.float32, (T, K)))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
