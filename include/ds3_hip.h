@@ -262,7 +262,7 @@ int ds3_hip_moe_block(
  * Same arguments, semantics and results as ds3_hip_moe_ffn_batch; every
  * intermediate (routing rows, bucketing lists, h, y) lives in one library-owned
  * scratch array of ds3_hip_noalloc_scratch_bytes() bytes per GPU (64 MiB: a
- * Qwen3-30B-A3B layer call of up to 1,285 tokens), held until the process ends.
+ * Qwen3-30B-A3B layer call of up to 1,284 tokens), held until the process ends.
  * A call whose intermediates do not fit returns -1 with a diagnostic; split it
  * into fewer tokens.  ds3_hip_init must have been called.  Every call on a GPU
  * shares that GPU's array: calls that overlap on one GPU (from several host

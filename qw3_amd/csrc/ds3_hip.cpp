@@ -1403,7 +1403,7 @@ int moe_batch(const float *x_in, const NormIn *norm, const ds3_hip_buffer_t *w_g
            o_h16 = 0, o_y = 0, o_rg = 0, o_rd = 0, o_dg = 0, o_dd = 0, o_mask = 0;
     int rpi_gu = 0, rpi_dn = 0;
     if (use_grouped) {
-        grouped_runs_per_tile((int)n_embd, (int)n_ff_exp, rpi_gu, rpi_dn);
+        grouped_runs_per_tile((int)n_embd, (int)n_ff_exp, (int)S, (int)n_expert, rpi_gu, rpi_dn);
         o_x16 = bp.take(T * n_embd * 2);
         o_cnt = bp.take((size_t)n_expert * 4);
         o_off = bp.take(((size_t)n_expert + 1) * 4);

@@ -203,9 +203,9 @@ bool grouped_type_ok(int type, int K);
 // n tile), n_ff a multiple of 128 and at most 1024 (down's token tile stays
 // in LDS).
 bool grouped_shape_ok(int n_embd, int n_ff);
-// n-runs per token tile of the grouped kernels for a layer shape (BucketOut
-// rpi_gu / rpi_dn).
-void grouped_runs_per_tile(int n_embd, int n_ff, int &rpi_gu, int &rpi_dn);
+// Runs per work item of the grouped kernels for a call of S slots over E
+// experts (gate_up's run length depends on how many runs the call makes).
+void grouped_runs_per_tile(int n_embd, int n_ff, int S, int E, int &rpi_gu, int &rpi_dn);
 
 // Dense C[M][N] = A W^T (fp16 operands, fp32 accumulate) on the grouped
 // gate_up kernel: x16 = A [M][K] in fp16; b = the bucketing lists of one

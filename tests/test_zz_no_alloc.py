@@ -66,16 +66,16 @@ def test_noalloc_refuses_oversized_call(hip_ready, layer, capfd):
 
 
 def test_noalloc_capacity_edge(hip_ready, layer):
-    """The documented capacity for a Qwen3-30B-A3B layer call: 1,285 tokens
-    fit the scratch array (and match the allocating entry point), 1,286 are
+    """The documented capacity for a Qwen3-30B-A3B layer call: 1,284 tokens
+    fit the scratch array (and match the allocating entry point), 1,285 are
     refused."""
     s = layer.spec
-    T = 1285
+    T = 1284
     print(f"  noalloc at its capacity, T={T}", flush=True)
     x = ds3.Buffer.from_array(W.make_inputs(2, T, seed=900))
     got, want = _run(layer, x, T, True), _run(layer, x, T, False)
     assert all(np.array_equal(g, w) for g, w in zip(got, want))
-    T = 1286
+    T = 1285
     print(f"  noalloc one token past it, T={T}", flush=True)
     x = ds3.Buffer.alloc(T * s.n_embd * 4)
     out = ds3.Buffer.alloc(T * s.n_embd * 4)
