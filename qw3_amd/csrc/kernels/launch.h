@@ -203,6 +203,8 @@ bool grouped_type_ok(int type, int K);
 // n tile), n_ff a multiple of 128 and at most 1024 (down's token tile stays
 // in LDS).
 bool grouped_shape_ok(int n_embd, int n_ff);
+// Compute units of the current device (queried once; 256 if the query fails).
+int device_cu_count();
 // Runs per work item of the grouped kernels for a call of S slots over E
 // experts (gate_up's run length depends on how many runs the call makes).
 void grouped_runs_per_tile(int n_embd, int n_ff, int S, int E, int &rpi_gu, int &rpi_dn);

@@ -864,7 +864,7 @@ bool grouped_shape_ok(int n_embd, int n_ff)
 #define DS3_DN_NTB 8
 #endif
 
-static int gg_cu_count()
+int device_cu_count()
 {
     static int n_cu = 0;
     if (n_cu == 0) {
@@ -885,7 +885,7 @@ static int gg_cu_count()
 void grouped_runs_per_tile(int n_embd, int n_ff, int S, int E, int &rpi_gu, int &rpi_dn)
 {
     const int n_nt = n_ff / GG_TILE_N, items = S / GG_TILE_M + E / 2;
-    const int ntb = (int64_t)items * ((n_nt + 2) / 3) <= gg_cu_count() ? 3 : 2;
+    const int ntb = (int64_t)items * ((n_nt + 2) / 3) <= device_cu_count() ? 3 : 2;
     rpi_gu = (n_nt + ntb - 1) / ntb;
     rpi_dn = (n_embd / GG_TILE_N + DS3_DN_NTB - 1) / DS3_DN_NTB;
 }
@@ -894,7 +894,7 @@ void grouped_runs_per_tile(int n_embd, int n_ff, int S, int E, int &rpi_gu, int 
 // run list cannot be that long.
 static unsigned gg_grid(int max_runs)
 {
-    const int n_cu = gg_cu_count();
+    const int n_cu = device_cu_count();
     const int g = (n_cu + N_XCD - 1) / N_XCD * N_XCD, need = (max_runs + N_XCD - 1) / N_XCD * N_XCD;
     return (unsigned)(need < g ? (need > 0 ? need : N_XCD) : g);
 }

@@ -863,9 +863,11 @@ hipError_t launch_router_seq(const float *x, int T, int K, int E, int rtype, con
     // 16-byte DMAs need 16-byte aligned rows; 4-byte ones take any float rows
     const bool vec = K % 4 == 0 && wstride % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
                      ((uintptr_t)x16 & 15) == 0;
-    // 4 stages (3 chunks in flight) while one workgroup per CU covers the
-    // tokens; 2 stages (two workgroups per CU) for long batches
-    const bool deep = (T + 15) / 16 * ((E + 15) / 16) <= 512;
+    // 4 stages (3 chunks in flight, one 133 KB workgroup per CU) while the
+    // grid fits one round of the CUs; past that 2 stages, two workgroups per
+    // CU in one round (MI355X, T=1024: 26.6 against 36.2 us with 4 stages in
+    // two rounds; T=768 25.3 against 34.9)
+    const bool deep = (int64_t)((T + 15) / 16) * ((E + 15) / 16) <= device_cu_count();
     RouteArgs none{};
     if (vec && x16 == nullptr && T <= 4) {
         // one token group: fuse top-k when the caller gave a ticket
