@@ -120,13 +120,14 @@ k_decode_gate_up(const float *__restrict__ x, int64_t ldx, const int32_t *__rest
 // paths carve the same dynamic LDS.
 // ---------------------------------------------------------------------------
 #ifndef DS3_DG_ROWS
-#define DS3_DG_ROWS 8
+#define DS3_DG_ROWS 4
 #endif
 #ifndef DS3_DG_WPC
-#define DS3_DG_WPC 2
+#define DS3_DG_WPC 3
 #endif
 constexpr int DG_R = DS3_DG_ROWS;                // rows per chunk, of gate and of up
 constexpr int DG_WPC = DS3_DG_WPC;               // workgroups per CU over all slots
+static_assert(DG_R >= 4 && DG_R % 4 == 0, "each of the 4 waves dots DG_R / 4 rows of a chunk");
 
 template <int GT, int UPL>
 struct DgChunk {
