@@ -31,10 +31,10 @@ namespace ds3k {
 bool gemv_type_ok(int type, int K);
 
 #ifndef DS3_G1_ROWS
-#define DS3_G1_ROWS 8               // rows per chunk at K = 2048 (half at 4096)
+#define DS3_G1_ROWS 4               // rows per chunk at K = 2048 (half at 4096, at least 4)
 #endif
 #ifndef DS3_G1_WPC
-#define DS3_G1_WPC 4                // persistent workgroups per CU
+#define DS3_G1_WPC 6                // persistent workgroups per CU
 #endif
 #ifndef DS3_G1_SETS
 #define DS3_G1_SETS 2               // register sets of chunks in flight per workgroup
@@ -43,7 +43,7 @@ bool gemv_type_ok(int type, int K);
 template <int TYPE, int UPL>
 struct G1 {
     static constexpr int RB = G1Row<TYPE>::RB * UPL;             // bytes per row
-    static constexpr int R = DS3_G1_ROWS / UPL;                  // rows per chunk
+    static constexpr int R = DS3_G1_ROWS / UPL < 4 ? 4 : DS3_G1_ROWS / UPL;   // rows per chunk (one per wave at least)
     static constexpr int CB = R * RB;                            // chunk bytes
     static constexpr int NL = (CB + G1_LOAD - 1) / G1_LOAD;      // 16-byte loads per thread and chunk
     static constexpr int BUF = NL * G1_LOAD;                     // LDS bytes per buffer
